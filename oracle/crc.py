@@ -1,0 +1,67 @@
+"""ctypes binding of oracle/lib/liboracle_rc.so (TEST INFRASTRUCTURE ONLY).
+
+The C range coder (oracle/range_coder.c) restates krunch_ac/cpu_reference.py
+and is pinned against oracle/range_coder.py in tests/test_oracle_rc.py.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+import numpy as np
+
+_LIB = None
+
+
+def lib():
+    global _LIB
+    if _LIB is None:
+        path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "lib", "liboracle_rc.so")
+        if not os.path.exists(path):
+            raise RuntimeError(f"{path} missing: run `make -C oracle`")
+        L = ctypes.CDLL(path)
+        P = ctypes.c_void_p
+        L.orc_encode_intervals.argtypes = [P, P, ctypes.c_size_t, ctypes.c_int, P, ctypes.c_size_t]
+        L.orc_encode_intervals.restype = ctypes.c_size_t
+        L.orc_decoder_size.restype = ctypes.c_size_t
+        L.orc_decoder_init.argtypes = [P, P, ctypes.c_uint64]
+        L.orc_decoder_target.argtypes = [P, ctypes.c_int]
+        L.orc_decoder_target.restype = ctypes.c_uint32
+        L.orc_decoder_consume.argtypes = [P, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_int]
+        L.orc_decode_rows.argtypes = [P, P, ctypes.c_size_t, ctypes.c_uint32, ctypes.c_int, P]
+        _LIB = L
+    return _LIB
+
+
+def encode_intervals(lo: np.ndarray, hi: np.ndarray, log2_total: int = 24) -> bytes:
+    lo = np.ascontiguousarray(lo, dtype=np.uint32)
+    hi = np.ascontiguousarray(hi, dtype=np.uint32)
+    cap = 4 * len(lo) + 64
+    while True:
+        out = np.zeros(cap, dtype=np.uint8)
+        n = lib().orc_encode_intervals(lo.ctypes.data, hi.ctypes.data, len(lo), log2_total,
+                                       out.ctypes.data, cap)
+        if n <= cap:
+            return out[:n].tobytes()
+        cap = n
+
+
+class Decoder:
+    def __init__(self, data: bytes, log2_total: int = 24):
+        self._data = np.frombuffer(data, dtype=np.uint8).copy()
+        self._st = ctypes.create_string_buffer(lib().orc_decoder_size())
+        self.log2_total = log2_total
+        lib().orc_decoder_init(self._st, self._data.ctypes.data, len(self._data))
+
+    def target(self) -> int:
+        return lib().orc_decoder_target(self._st, self.log2_total)
+
+    def consume(self, lo: int, hi: int):
+        lib().orc_decoder_consume(self._st, lo, hi, self.log2_total)
+
+    def decode_rows(self, cdf: np.ndarray) -> np.ndarray:
+        cdf = np.ascontiguousarray(cdf, dtype=np.uint32)
+        out = np.empty(cdf.shape[0], dtype=np.int32)
+        lib().orc_decode_rows(self._st, cdf.ctypes.data, cdf.shape[0], cdf.shape[1] - 1,
+                              self.log2_total, out.ctypes.data)
+        return out

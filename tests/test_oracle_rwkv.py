@@ -1,0 +1,57 @@
+"""Forward oracle: the WKV recurrence against its closed form, T=1 from the
+initial state, and the packed == stepped / windowed == single invariants."""
+import numpy as np
+import torch
+
+from oracle import rwkv4
+from tests.golden import make_golden as mg
+
+
+def _direct_wkv(k, v, w, u):
+    """y_t = (sum_{i<t} e^{(t-1-i)w + k_i} v_i + e^{u+k_t} v_t) / (same without v)."""
+    B, T, C = k.shape
+    k, v, w, u = (a.double() for a in (k, v, w, u))
+    y = torch.empty(B, T, C, dtype=torch.float64)
+    for t in range(T):
+        i = torch.arange(t, dtype=torch.float64)
+        wt = torch.exp((t - 1 - i)[None, :, None] * w + k[:, :t])
+        cur = torch.exp(u + k[:, t])
+        y[:, t] = ((wt * v[:, :t]).sum(1) + cur * v[:, t]) / (wt.sum(1) + cur)
+    return y
+
+
+def test_wkv_closed_form():
+    g = torch.Generator().manual_seed(0)
+    B, T, C = 3, 40, 16
+    k = torch.randn(B, T, C, generator=g) * 2
+    v = torch.randn(B, T, C, generator=g)
+    w = -torch.exp(torch.linspace(-5, 3, C))
+    u = torch.full((C,), float(np.log(0.3)))
+    st = rwkv4.new_state(1, B, C)[0]
+    y = rwkv4.wkv(k, v, w, u, st)
+    np.testing.assert_allclose(y.numpy(), _direct_wkv(k, v, w, u).numpy(), rtol=2e-5, atol=2e-6)
+
+
+def test_wkv_first_step_is_v():
+    g = torch.Generator().manual_seed(1)
+    k, v = torch.randn(2, 1, 8, generator=g), torch.randn(2, 1, 8, generator=g)
+    st = rwkv4.new_state(1, 2, 8)[0]
+    y = rwkv4.wkv(k, v, -torch.ones(8), torch.zeros(8), st)
+    torch.testing.assert_close(y, v, rtol=0, atol=1e-7)
+
+
+def test_packed_equals_stepped_rowwise_and_windowed():
+    t = mg.TINY
+    w = mg.tiny_weights(**t)
+    ids = torch.as_tensor(mg.tiny_ids(**t))
+    T = ids.shape[1]
+    st_p = rwkv4.new_state(t["n_layer"], t["B"], t["C"])
+    packed = rwkv4.forward(w, ids, st_p, rowwise=True)
+    st_s = rwkv4.new_state(t["n_layer"], t["B"], t["C"])
+    stepped = torch.cat([rwkv4.forward(w, ids[:, i:i + 1], st_s, rowwise=True)
+                         for i in range(T)], dim=1)
+    assert torch.equal(packed, stepped)
+    st_w = rwkv4.new_state(t["n_layer"], t["B"], t["C"])
+    windowed = torch.cat([rwkv4.forward(w, ids[:, :3], st_w, rowwise=True),
+                          rwkv4.forward(w, ids[:, 3:], st_w, rowwise=True)], dim=1)
+    assert torch.equal(packed, windowed)
