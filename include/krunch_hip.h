@@ -1,0 +1,245 @@
+/*
+ * krunch_hip.h — C ABI of libkrunch_hip.so, the MI355X (gfx950) engine for
+ * krunch's batched RWKV-4 compress/decompress path.
+ *
+ * Conventions (all entry points):
+ *   - device pointers and plain sizes only; `stream` is a hipStream_t (NULL =
+ *     the default stream); launches are asynchronous, nothing synchronises
+ *     unless stated;
+ *   - return 0 on success, a negative code on failure; kr_last_error() gives
+ *     the message (thread-local);
+ *   - the caller owns every buffer; coder states and RNN states are mutated
+ *     in place (as the reference's ops do, krunch_ac/cuda/main.cpp:111-130);
+ *   - fp16 tensors are passed as uint16_t bit patterns;
+ *   - cdf_precision is log2 of the CDF total (24 in the reference,
+ *     krunch_ac/cdf.py:18-19; range_coder.cuh:19-20).
+ *
+ * Each declaration names the reference interface it replaces.
+ */
+#ifndef KRUNCH_HIP_H
+#define KRUNCH_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---------------------------------------------------------------- errors */
+const char* kr_last_error(void);
+int kr_abi_version(void);
+
+/* ------------------------------------------------------------ range coder
+ * Coder state: 4 x uint32 per stream, {low, high, pending, bit_offset} for
+ * encoding and {low, high, value, bit_offset} for decoding
+ * (range_coder.cuh:24-40). Encoders start from {0, 0xFFFFFFFF, 0, 0} and OR
+ * bits into a zero-filled output buffer; out_cap bounds every write (an
+ * overflow sets *err_flag, which may be NULL). Decoders read zero bits past
+ * the end of a stream: in_len bounds the whole input buffer, byte_limits
+ * (nullable) each stream's own length. base_byte_offsets (nullable where
+ * noted) gives each stream's first byte.
+ */
+
+/* replaces krunch_ac_cuda.encode_step (main.cpp encode_step; encode_kernel.cu:53-101):
+ * N rows of one stream, full CDF rows of cdf_stride int32 entries. */
+int kr_encode_step(const int32_t* cdf, int cdf_stride, const int32_t* symbols, int N,
+                   uint8_t* output_buf, uint32_t out_cap, uint32_t* state, int cdf_precision,
+                   uint32_t* err_flag, void* stream);
+
+/* replaces krunch_ac_cuda.encode_finalize (encode_kernel.cu:106-119). */
+int kr_encode_finalize(uint8_t* output_buf, uint32_t out_cap, uint32_t* state,
+                       uint32_t* err_flag, void* stream);
+
+/* replaces krunch_ac_cuda.encode_step_batched (encode_kernel.cu:148-197):
+ * one symbol per stream, CDF rows [B, V+1]. */
+int kr_encode_step_batched(const int32_t* cdfs, int V, const int32_t* symbols,
+                           uint8_t* output_buf, uint32_t out_cap,
+                           const int32_t* base_byte_offsets, uint32_t* states, int B,
+                           int cdf_precision, uint32_t* err_flag, void* stream);
+
+/* Fused-compress form of encode_step_batched over T steps: pairs[b*pair_stride+t]
+ * = (cdf[sym], cdf[sym+1]) as produced by kr_softmax_cdf_pairs; stream b encodes
+ * its first n_valid[b] rows (n_valid nullable = T). No reference counterpart: the
+ * reference writes full [rows, V+1] CDFs and reads two entries per row
+ * (cpp_path.py:499-500 + encode_kernel.cu:110-111). */
+int kr_encode_pairs_batched(const uint32_t* pairs, int T, long long pair_stride,
+                            const int32_t* n_valid, uint8_t* output_buf, uint32_t out_cap,
+                            const int32_t* base_byte_offsets, uint32_t* states, int B,
+                            int cdf_precision, uint32_t* err_flag, void* stream);
+
+/* replaces krunch_ac_cuda.encode_finalize_batched (encode_kernel.cu:199-215);
+ * base_byte_offsets nullable (all streams at offset 0 is then B = 1). */
+int kr_encode_finalize_batched(uint8_t* output_buf, uint32_t out_cap,
+                               const int32_t* base_byte_offsets, uint32_t* states, int B,
+                               uint32_t* err_flag, void* stream);
+
+/* replaces krunch_ac_cuda.decode_init_batched and, with B = 1 and NULL offsets,
+ * decode_init (decode_kernel.cu:28-45,138-157). */
+int kr_decode_init_batched(const uint8_t* input_buf, uint32_t in_len,
+                           const int32_t* base_byte_offsets, const int32_t* byte_limits,
+                           uint32_t* states, int B, void* stream);
+
+/* replaces krunch_ac_cuda.decode_step_batched and, with B = 1, decode_step
+ * (decode_kernel.cu:50-110,159-216): CDF rows [B, V+1] -> out_syms [B]. */
+int kr_decode_step_batched(const int32_t* cdfs, int V, const uint8_t* input_buf,
+                           uint32_t in_len, const int32_t* base_byte_offsets,
+                           const int32_t* byte_limits, uint32_t* states, int32_t* out_syms,
+                           int B, int cdf_precision, void* stream);
+
+/* -------------------------------------------------------------------- CDF
+ * One 1024-thread workgroup per row; V <= 65536. Probabilities are
+ * renormalised with numpy's float32 summation order, so results are
+ * bit-identical to krunch_ac/cdf.py:22-74. Softmax of fp16 logits (row
+ * stride ld elements): e = exp(x - max) with a fixed exp2-based routine,
+ * q = e * (1 / sum e), then cdf.py on q.
+ */
+
+/* replaces krunch_ac.probs_to_cdf (cdf.py:22-74) / probs_to_cdf_gpu
+ * (gpu_encode.py:22-48): float probs [N, ld] -> uint32 cdf [N, V+1]. */
+int kr_probs_to_cdf(const float* probs, int N, int V, long long ld, uint32_t* cdf_out,
+                    int cdf_precision, void* stream);
+
+/* replaces krunch_ac_cuda.det_softmax_cdf (det_softmax_cdf.cu:62-195) and the
+ * caller's cumsum (cpp_path.softmax_cdfs_per_row, :490-501): out [N, V+1] int32
+ * holds the cumulative CDF (cumulative = 1) or 0 followed by the per-symbol
+ * counts (cumulative = 0, the reference op's output). */
+int kr_softmax_cdf(const uint16_t* logits, int N, int V, long long ld, int32_t* out,
+                   int cumulative, int cdf_precision, void* stream);
+
+/* The softmax probabilities q [N, V] fed to the CDF (test and inspection aid;
+ * the reference's torch.softmax in inference.py:254 plays this role). */
+int kr_softmax_probs(const uint16_t* logits, int N, int V, long long ld, float* probs,
+                     void* stream);
+
+/* Fused compress stage: per row only the interval of symbols[row],
+ * pairs[row] = (cdf[sym], cdf[sym+1]) — replaces det_softmax_cdf + cumsum +
+ * the coder's two reads (cpp_path.py:499-500, encode_kernel.cu:110-111). */
+int kr_softmax_cdf_pairs(const uint16_t* logits, int N, int V, long long ld,
+                         const int32_t* symbols, uint32_t* pairs, int cdf_precision,
+                         void* stream);
+
+/* Fused decompress stage for B streams (one row of logits each): CDF, search
+ * for the decoder target, range decode; writes out_syms[b] and, if tokens is
+ * given, tokens[b*tok_stride + tok_count[b]++]. Streams with
+ * tok_count[b] >= n_tokens[b] are skipped (n_tokens nullable). Replaces
+ * softmax_cdfs_per_row + decode_step_batched (inference.py:427-431). */
+int kr_softmax_cdf_decode(const uint16_t* logits, int B, int V, long long ld,
+                          const uint8_t* input_buf, uint32_t in_len,
+                          const int32_t* base_byte_offsets, const int32_t* byte_limits,
+                          uint32_t* states, int32_t* out_syms, int32_t* tokens,
+                          long long tok_stride, int32_t* tok_count, const int32_t* n_tokens,
+                          int cdf_precision, void* stream);
+
+/* ------------------------------------------------------------ GEMM / model
+ * Matrices of the model are stored transposed, [out, in] (K contiguous).
+ * Every output element is one chain of v_mfma_f32_16x16x32_f16 over K in
+ * increasing order starting from 0, so results do not depend on M.
+ */
+
+/* W [K, N] (row stride ldw) -> Wt [N, K] (row stride ldt), fp16. */
+int kr_transpose_f16(const uint16_t* W, long long ldw, int K, int N, uint16_t* Wt,
+                     long long ldt, void* stream);
+
+/* replaces krunch_ac_cuda.det_matmul (layer_cpp.cpp:728-822, det_matmul_tc*.cu):
+ * out = epilogue(x [M,K] @ W) with W given as Wt [N, ldw]. epilogue: 0 fp32 out,
+ * 1 fp16 out, 2 fp16 sigmoid, 3 fp16 relu^2, 4 fp16 res + acc, 5 fp16
+ * res + gate * acc (res/gate [M, ldo] fp16, res may alias out). */
+int kr_det_matmul(const uint16_t* x, int M, int K, const uint16_t* Wt, long long ldw, int N,
+                  void* out, long long ldo, int epilogue, const uint16_t* res,
+                  const uint16_t* gate, void* stream);
+
+typedef struct kr_layer_weights {
+    const void *ln1_w, *ln1_b;            /* fp16 [C] */
+    const void *tm_k, *tm_v, *tm_r;       /* fp16 [C] */
+    const float *decay;                   /* fp32 [C], w = -exp(time_decay_raw) */
+    const float *first;                   /* fp32 [C], u = time_first */
+    const void *Kt, *Vt, *Rt, *Ot;        /* fp16 [C, C] */
+    const void *ln2_w, *ln2_b;            /* fp16 [C] */
+    const void *ftm_k, *ftm_r;            /* fp16 [C] */
+    const void *fKt;                      /* fp16 [F, C] */
+    const void *fVt;                      /* fp16 [C, F] */
+    const void *fRt;                      /* fp16 [C, C] */
+} kr_layer_weights;
+
+typedef struct kr_model_weights {
+    int n_layer, C, F, V;                 /* C in {256,512,768,1024}, F % 64 == 0, V <= 65536 */
+    const void* emb;                      /* fp16 [V, C] */
+    const void *ln_out_w, *ln_out_b;      /* fp16 [C] */
+    const void* headT;                    /* fp16 [V, C] */
+    const kr_layer_weights* layers;       /* host array, n_layer entries */
+} kr_model_weights;
+
+/* w = -exp(raw) for the WKV decay (the rwkv loader's transform the reference
+ * relies on, wkv_kernel.cu:41-45). */
+int kr_prepare_decay(const float* raw, float* out, int n, void* stream);
+
+/* RNN state of B streams for n_layer layers in one buffer; per layer
+ * [att_xx fp16 | ffn_xx fp16 | aa | bb | pp fp32], each [B, C]
+ * (cpp_path.fresh_state_batched, cpp_path.py:412-425). */
+size_t kr_state_bytes(int n_layer, int B, int C);
+/* att_xx = ffn_xx = aa = bb = 0, pp = -1e30 (fill kernel, graph-safe). */
+int kr_state_init(void* state, int n_layer, int B, int C, void* stream);
+
+/* Scratch needed by the layer stack for M = B*T rows. */
+size_t kr_forward_workspace_bytes(long long M, int C, int F);
+
+/* replaces krunch_ac_cuda.rwkv4_layer_step_cpp / _t1 (layer_cpp.cpp:294-637):
+ * one layer over x [B*T, C] fp16 in place, state tensors [B, C] mutated. */
+int kr_layer_step(const kr_layer_weights* L, int C, int F, void* x, int B, int T,
+                  void* att_xx, float* aa, float* bb, float* pp, void* ffn_xx, void* ws,
+                  size_t ws_bytes, void* stream);
+
+/* replaces launch_krunch_wkv_forward (wkv_kernel.cu:75-92), fused with the
+ * receptance: ry = fp16(r * fp16(y)); k, v fp32 [B*T, C], r/ry fp16. */
+int kr_wkv(int B, int T, int C, const float* decay, const float* first, const float* k,
+           const float* v, const uint16_t* r, float* aa, float* bb, float* pp, uint16_t* ry,
+           void* stream);
+
+/* All layers over x [B*T, C] (cpp_path.forward_packed_window's layer loop,
+ * :155-160; forward_stepped_batched's with T = 1, :451-456). */
+int kr_forward_layers(const kr_model_weights* m, void* x, int B, int T, void* state, void* ws,
+                      size_t ws_bytes, void* stream);
+
+/* x[row] = emb[ids[row]] (cpp_path.py:154,450). */
+int kr_embed(const kr_model_weights* m, const int32_t* ids, int M, void* x, void* stream);
+
+/* logits [M, ld] fp16 = LN_out(x) @ head (cpp_path.py:161-163); xn: [M, C] scratch. */
+int kr_head_logits(const kr_model_weights* m, const void* x, int M, void* xn, void* logits,
+                   long long ld, void* stream);
+
+/* One packed compress window for B streams x T tokens (rows b*T + t): embed,
+ * layers, then per block of head_rows rows head logits -> softmax -> symbol
+ * interval into pairs [B*T, 2]. Replaces the per-window body of
+ * InferenceEngine._compress_chunk_cpp (inference.py:331-338). Encode the pairs
+ * with kr_encode_pairs_batched. */
+int kr_compress_window(const kr_model_weights* m, const int32_t* inputs, const int32_t* targets,
+                       int B, int T, void* state, void* x, void* ws, size_t ws_bytes,
+                       void* logits, long long ld, int head_rows, uint32_t* pairs,
+                       int cdf_precision, void* stream);
+
+/* One stepped decompress step for B streams: embed syms, layers (T = 1), head,
+ * fused CDF + range decode; syms is read (previous tokens) and overwritten
+ * (decoded tokens). Replaces one iteration of the loop in
+ * _decompress_chunks_batched_cpp (inference.py:427-434). */
+int kr_decode_step(const kr_model_weights* m, int B, void* state, int32_t* syms, void* x,
+                   void* ws, size_t ws_bytes, void* logits, long long ld,
+                   const uint8_t* input_buf, uint32_t in_len, const int32_t* base_byte_offsets,
+                   const int32_t* byte_limits, uint32_t* ac_states, int32_t* tokens,
+                   long long tok_stride, int32_t* tok_count, const int32_t* n_tokens,
+                   int cdf_precision, void* stream);
+
+/* n_steps decode steps; with use_graph the step is captured once into a HIP
+ * graph and replayed (the reference's graph path, cpp_path.py:229-276).
+ * Synchronous with respect to the work it enqueues. */
+int kr_decode_run(const kr_model_weights* m, int B, void* state, int32_t* syms, void* x,
+                  void* ws, size_t ws_bytes, void* logits, long long ld,
+                  const uint8_t* input_buf, uint32_t in_len, const int32_t* base_byte_offsets,
+                  const int32_t* byte_limits, uint32_t* ac_states, int32_t* tokens,
+                  long long tok_stride, int32_t* tok_count, const int32_t* n_tokens,
+                  int cdf_precision, int n_steps, int use_graph, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* KRUNCH_HIP_H */

@@ -1,0 +1,628 @@
+// Row-wise probabilities -> integer CDF on the GPU, bit-exact with the spec
+// krunch_ac/cdf.py:22-74, optionally preceded by the deterministic softmax
+// of fp16 logits (the role of det_softmax_cdf.cu:62-185 in the reference).
+//
+// One 1024-thread workgroup per row. The row's values live in registers in
+// the layout of numpy's float32 pairwise summation: the row is split into
+// 8192-element blocks, each block recursively halved (split rounded down to a
+// multiple of 8) into leaves of <= 128 elements; a leaf is summed by 8
+// interleaved accumulators (element i goes to accumulator i % 8), the 8
+// accumulators are combined as ((a0+a1)+(a2+a3))+((a4+a5)+(a6+a7)) and the
+// len % 8 tail is added in order. One group of 8 lanes owns one leaf (lane j
+// holds accumulator j's elements plus tail element j), so the 8-way combine
+// is an xor-butterfly over lanes 1, 2, 4. Inner nodes of the recursion are
+// combined level by level in LDS from a host-built plan; block sums are added
+// left to right onto 0. The result equals numpy's `p.sum(axis=1)` bit for
+// bit, which cdf.py uses to renormalise.
+//
+// Modes: materialise the CDF (or per-symbol counts, the reference's
+// det_softmax_cdf output), write the probabilities, emit only the
+// (cdf[sym], cdf[sym+1]) interval of a given symbol per row (compress), or
+// find the symbol whose interval contains a range decoder's target and
+// advance the decoder (decompress, fused).
+#include <cstring>
+#include <map>
+#include <mutex>
+#include <vector>
+#include <algorithm>
+
+#include "kr_math.h"
+#include "kr_rc_device.h"
+
+namespace {
+
+constexpr int kThreads = 1024;
+constexpr int kWaves = kThreads / 64;
+constexpr int kLeavesPerIt = kWaves * 8;     // 128 leaves per register slice
+constexpr int kMaxIt = 4;                    // up to 512 leaves: V <= 65536
+constexpr int kMaxLeaves = kMaxIt * kLeavesPerIt;
+constexpr int kMaxNodes = 2 * kMaxLeaves;
+
+enum : int { IN_LOGITS_F16 = 0, IN_PROBS_F32 = 1 };
+enum : int { M_CDF = 0, M_COUNTS = 1, M_PROBS = 2, M_PAIRS = 3, M_DECODE = 4 };
+
+struct PlanArgs {
+    const int2* leaves;      // (start, len), index order
+    const int2* inner;       // (left, right) node ids, grouped by level
+    const int* level_start;  // n_levels + 1 offsets into inner
+    const int* roots;        // node id of each 8192-block
+    int V, n_leaves, n_inner, n_levels, n_blocks;
+};
+
+struct DecodeArgs {
+    const uint8_t* in;
+    uint32_t in_len;
+    const int32_t* base;      // per-stream byte offset (nullable -> 0)
+    const int32_t* limits;    // per-stream byte length (nullable)
+    kr_rc_state* states;
+    int32_t* out_syms;        // [B] symbol decoded this step
+    int32_t* tokens;          // [B, tok_stride] decoded tokens (nullable)
+    long long tok_stride;
+    int32_t* tok_count;       // [B] tokens written so far (nullable)
+    const int32_t* n_tokens;  // [B] stream length; finished streams are skipped (nullable)
+};
+
+struct RowShared {
+    float node[kMaxNodes];
+    int leaf_count[kMaxLeaves];
+    int leaf_buf[128];
+    float redf[kWaves];
+    float redp[kWaves];
+    int redi[kWaves];
+    int redi2[kWaves];
+    int redi3[kWaves];
+    int redL[kWaves];
+    float total;
+    int amax, deficit, amax_leaf, hit_leaf, hit_start, hit_len;
+    uint32_t target, hit_prefix;
+};
+
+__device__ __forceinline__ float wave_max(float v) {
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+    return v;
+}
+__device__ __forceinline__ int wave_isum(int v) {
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    return v;
+}
+// (value desc, index asc) total order: the first maximum wins.
+__device__ __forceinline__ bool better(float pv, int pi, float bv, int bi) {
+    return pv > bv || (pv == bv && pi < bi);
+}
+
+template <int IN>
+__device__ __forceinline__ float load_val(const void* row, int i) {
+    if constexpr (IN == IN_LOGITS_F16) return (float)reinterpret_cast<const kr_half*>(row)[i];
+    else return reinterpret_cast<const float*>(row)[i];
+}
+
+// Sum of all held values in numpy's order (see file header). Every thread
+// returns the same value.
+__device__ float row_sum_numpy(float (&v)[kMaxIt][17], const int (&nfull)[kMaxIt],
+                               const int (&rem)[kMaxIt], const int (&len)[kMaxIt],
+                               const PlanArgs& P, RowShared& sh, int lane, int wave) {
+    const int grp = lane >> 3, j = lane & 7;
+    #pragma unroll
+    for (int it = 0; it < kMaxIt; it++) {
+        float r = v[it][0];
+        #pragma unroll
+        for (int k = 1; k < 16; k++)
+            if (k < nfull[it]) r = r + v[it][k];
+        r = r + __shfl_xor(r, 1);
+        r = r + __shfl_xor(r, 2);
+        r = r + __shfl_xor(r, 4);
+        float res = len[it] >= 8 ? r : -0.0f;
+        #pragma unroll
+        for (int t = 0; t < 7; t++) {
+            const float tv = __shfl(v[it][16], (grp << 3) + t);
+            if (t < rem[it]) res = res + tv;
+        }
+        const int L = it * kLeavesPerIt + wave * 8 + grp;
+        if (j == 0 && L < P.n_leaves) sh.node[L] = res;
+    }
+    __syncthreads();
+    for (int lev = 0; lev < P.n_levels; lev++) {
+        const int s = P.level_start[lev], e = P.level_start[lev + 1];
+        for (int idx = s + (int)threadIdx.x; idx < e; idx += kThreads) {
+            const int2 ch = P.inner[idx];
+            sh.node[P.n_leaves + idx] = sh.node[ch.x] + sh.node[ch.y];
+        }
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) {
+        float acc = 0.0f;
+        for (int b = 0; b < P.n_blocks; b++) acc = acc + sh.node[P.roots[b]];
+        sh.total = acc;
+    }
+    __syncthreads();
+    return sh.total;
+}
+
+template <int IN, int MODE>
+__global__ void __launch_bounds__(kThreads)
+row_cdf_kernel(const void* __restrict__ input, long long ld, int n_rows, PlanArgs P, int prec,
+               void* __restrict__ out, long long out_ld, const int32_t* __restrict__ symbols,
+               DecodeArgs D) {
+    __shared__ RowShared sh;
+    const int row = blockIdx.x;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int grp = lane >> 3, j = lane & 7;
+    const int V = P.V;
+
+    if constexpr (MODE == M_DECODE) {
+        // Finished streams do nothing this step (uniform per workgroup).
+        if (D.n_tokens && D.tok_count && D.tok_count[row] >= D.n_tokens[row]) return;
+        if (tid == 0) {
+            const kr_rc_state st = D.states[row];
+            sh.target = kr_rc_target(st.low, st.high, st.pending_or_value, prec);
+            sh.hit_leaf = -1;
+        }
+    }
+
+    const char* rowp;
+    if constexpr (IN == IN_LOGITS_F16)
+        rowp = reinterpret_cast<const char*>(input) + (size_t)row * (size_t)ld * 2;
+    else
+        rowp = reinterpret_cast<const char*>(input) + (size_t)row * (size_t)ld * 4;
+
+    // ---- gather the row into registers, leaf layout ----
+    float v[kMaxIt][17];
+    int start[kMaxIt], len[kMaxIt], nfull[kMaxIt], rem[kMaxIt];
+    #pragma unroll
+    for (int it = 0; it < kMaxIt; it++) {
+        const int L = it * kLeavesPerIt + wave * 8 + grp;
+        int2 lf = make_int2(0, 0);
+        if (L < P.n_leaves) lf = P.leaves[L];
+        start[it] = lf.x;
+        len[it] = lf.y;
+        nfull[it] = lf.y >= 8 ? (lf.y >> 3) : 0;
+        rem[it] = lf.y >= 8 ? (lf.y & 7) : lf.y;
+        #pragma unroll
+        for (int k = 0; k < 16; k++)
+            v[it][k] = k < nfull[it] ? load_val<IN>(rowp, lf.x + j + 8 * k) : -INFINITY;
+        v[it][16] = j < rem[it] ? load_val<IN>(rowp, lf.x + 8 * nfull[it] + j) : -INFINITY;
+    }
+
+    float inv_S = 1.0f;
+    if constexpr (IN == IN_LOGITS_F16) {
+        // ---- row max (exact, order-free) ----
+        float m = -INFINITY;
+        #pragma unroll
+        for (int it = 0; it < kMaxIt; it++)
+            #pragma unroll
+            for (int k = 0; k < 17; k++) m = fmaxf(m, v[it][k]);
+        m = wave_max(m);
+        if (lane == 0) sh.redf[wave] = m;
+        __syncthreads();
+        m = sh.redf[0];
+        #pragma unroll
+        for (int w = 1; w < kWaves; w++) m = fmaxf(m, sh.redf[w]);
+        // ---- e = kexp(x - m); S = numpy-order sum; q = e * (1/S) ----
+        #pragma unroll
+        for (int it = 0; it < kMaxIt; it++)
+            #pragma unroll
+            for (int k = 0; k < 17; k++) v[it][k] = kr_kexp(__fsub_rn(v[it][k], m));
+        const float S = row_sum_numpy(v, nfull, rem, len, P, sh, lane, wave);
+        inv_S = 1.0f / S;
+        #pragma unroll
+        for (int it = 0; it < kMaxIt; it++)
+            #pragma unroll
+            for (int k = 0; k < 17; k++) v[it][k] = __fmul_rn(v[it][k], inv_S);
+    } else {
+        #pragma unroll
+        for (int it = 0; it < kMaxIt; it++)
+            #pragma unroll
+            for (int k = 0; k < 17; k++) if (v[it][k] == -INFINITY) v[it][k] = 0.0f;
+    }
+
+    if constexpr (MODE == M_PROBS) {
+        float* o = reinterpret_cast<float*>(out) + (size_t)row * (size_t)out_ld;
+        #pragma unroll
+        for (int it = 0; it < kMaxIt; it++) {
+            #pragma unroll
+            for (int k = 0; k < 16; k++)
+                if (k < nfull[it]) o[start[it] + j + 8 * k] = v[it][k];
+            if (j < rem[it]) o[start[it] + 8 * nfull[it] + j] = v[it][16];
+        }
+        return;
+    }
+
+    // ---- cdf.py: p = q / max(sum(q), 1e-30) ----
+    const float P_sum = row_sum_numpy(v, nfull, rem, len, P, sh, lane, wave);
+    const float denom = fmaxf(P_sum, 1e-30f);
+    const float scale = (float)((1 << prec) - V);
+
+    int sym = -1;
+    if constexpr (MODE == M_PAIRS) sym = symbols[row];
+
+    float bp = -1.0f;
+    int bi = 0x7fffffff, bL = 0;
+    int csum = 0, cpre = 0, csym = 0;
+    int32_t* orow = nullptr;
+    if constexpr (MODE == M_CDF || MODE == M_COUNTS)
+        orow = reinterpret_cast<int32_t*>(out) + (size_t)row * (size_t)out_ld;
+
+    #pragma unroll
+    for (int it = 0; it < kMaxIt; it++) {
+        const int L = it * kLeavesPerIt + wave * 8 + grp;
+        int lsum = 0;
+        #pragma unroll
+        for (int k = 0; k < 17; k++) {
+            const bool live = k < 16 ? (k < nfull[it]) : (j < rem[it]);
+            const int idx = k < 16 ? start[it] + j + 8 * k : start[it] + 8 * nfull[it] + j;
+            const float p = v[it][k] / denom;
+            const int c = (int)floorf(__fmul_rn(p, scale)) + 1;
+            if (live) {
+                if (better(p, idx, bp, bi)) { bp = p; bi = idx; bL = L; }
+                csum += c;
+                lsum += c;
+                if constexpr (MODE == M_CDF || MODE == M_COUNTS) orow[idx + 1] = c;
+                if constexpr (MODE == M_PAIRS) {
+                    if (idx < sym) cpre += c;
+                    if (idx == sym) csym = c;
+                }
+            }
+            if constexpr (MODE == M_DECODE) v[it][k] = __int_as_float(live ? c : 0);
+        }
+        if constexpr (MODE == M_DECODE) {
+            lsum += __shfl_xor(lsum, 1);
+            lsum += __shfl_xor(lsum, 2);
+            lsum += __shfl_xor(lsum, 4);
+            if (j == 0 && L < P.n_leaves) sh.leaf_count[L] = lsum;
+        }
+    }
+
+    // ---- argmax (first maximum) and integer sums across the workgroup ----
+    for (int o = 32; o > 0; o >>= 1) {
+        const float ov = __shfl_xor(bp, o);
+        const int oi = __shfl_xor(bi, o);
+        const int oL = __shfl_xor(bL, o);
+        if (better(ov, oi, bp, bi)) { bp = ov; bi = oi; bL = oL; }
+    }
+    csum = wave_isum(csum);
+    if constexpr (MODE == M_PAIRS) {
+        cpre = wave_isum(cpre);
+        csym = wave_isum(csym);
+    }
+    if (lane == 0) {
+        sh.redp[wave] = bp;
+        sh.redi[wave] = bi;
+        sh.redL[wave] = bL;
+        sh.redi2[wave] = csum;
+        if constexpr (MODE == M_PAIRS) sh.redi3[wave] = cpre;
+        if constexpr (MODE == M_PAIRS) sh.redf[wave] = __int_as_float(csym);
+    }
+    __syncthreads();
+    if (tid == 0) {
+        float gp = sh.redp[0];
+        int gi = sh.redi[0], gL = sh.redL[0], gs = sh.redi2[0];
+        for (int w = 1; w < kWaves; w++) {
+            if (better(sh.redp[w], sh.redi[w], gp, gi)) { gp = sh.redp[w]; gi = sh.redi[w]; gL = sh.redL[w]; }
+            gs += sh.redi2[w];
+        }
+        // A row with no finite maximum (NaN input) has no argmax; bin 0 then
+        // takes the deficit so every index stays in bounds.
+        if (gi < 0 || gi >= V) { gi = 0; gL = 0; }
+        const int deficit = (1 << prec) - gs;
+        sh.amax = gi;
+        sh.deficit = deficit;
+        sh.amax_leaf = gL;
+        if constexpr (MODE == M_CDF || MODE == M_COUNTS) {
+            orow[gi + 1] += deficit;
+            orow[0] = 0;
+        }
+        if constexpr (MODE == M_PAIRS) {
+            int pre = 0, cs = 0;
+            for (int w = 0; w < kWaves; w++) { pre += sh.redi3[w]; cs += __float_as_int(sh.redf[w]); }
+            const uint32_t lo = (uint32_t)(pre + (gi < sym ? deficit : 0));
+            const uint32_t wdt = (uint32_t)(cs + (gi == sym ? deficit : 0));
+            reinterpret_cast<uint2*>(out)[row] = make_uint2(lo, lo + wdt);
+        }
+        if constexpr (MODE == M_DECODE) sh.leaf_count[gL] += deficit;
+    }
+    if constexpr (MODE == M_PAIRS || MODE == M_COUNTS) return;
+
+    if constexpr (MODE == M_CDF) {
+        // Inclusive scan of counts over contiguous per-thread segments.
+        __syncthreads();
+        const int seg = (V + kThreads - 1) / kThreads;
+        const int i0 = min(V, tid * seg), i1 = min(V, i0 + seg);
+        int local = 0;
+        for (int i = i0; i < i1; i++) local += orow[i + 1];
+        int incl = local;
+        for (int o = 1; o < 64; o <<= 1) {
+            const int up = __shfl_up(incl, o);
+            if (lane >= o) incl += up;
+        }
+        if (lane == 63) sh.redi[wave] = incl;
+        __syncthreads();
+        int base = incl - local;
+        for (int w = 0; w < wave; w++) base += sh.redi[w];
+        for (int i = i0; i < i1; i++) {
+            base += orow[i + 1];
+            orow[i + 1] = base;
+        }
+        return;
+    }
+
+    if constexpr (MODE == M_DECODE) {
+        __syncthreads();
+        const uint32_t target = sh.target;
+        if (wave == 0) {
+            // exclusive scan over leaf totals; 8 consecutive leaves per lane
+            int loc[8];
+            int s = 0;
+            #pragma unroll
+            for (int q = 0; q < 8; q++) {
+                const int L = lane * 8 + q;
+                loc[q] = L < P.n_leaves ? sh.leaf_count[L] : 0;
+                s += loc[q];
+            }
+            int incl = s;
+            for (int o = 1; o < 64; o <<= 1) {
+                const int up = __shfl_up(incl, o);
+                if (lane >= o) incl += up;
+            }
+            uint32_t run = (uint32_t)(incl - s);
+            #pragma unroll
+            for (int q = 0; q < 8; q++) {
+                const int L = lane * 8 + q;
+                if (L < P.n_leaves && run <= target && target < run + (uint32_t)loc[q]) {
+                    sh.hit_leaf = L;
+                    sh.hit_prefix = run;
+                }
+                run += (uint32_t)loc[q];
+            }
+        }
+        __syncthreads();
+        const int Lstar = sh.hit_leaf;
+        const int gi = sh.amax, deficit = sh.deficit;
+        #pragma unroll
+        for (int it = 0; it < kMaxIt; it++) {
+            const int L = it * kLeavesPerIt + wave * 8 + grp;
+            if (L == Lstar) {
+                #pragma unroll
+                for (int k = 0; k < 17; k++) {
+                    const bool live = k < 16 ? (k < nfull[it]) : (j < rem[it]);
+                    const int off = k < 16 ? j + 8 * k : 8 * nfull[it] + j;
+                    if (live) {
+                        const int c = __float_as_int(v[it][k]);
+                        sh.leaf_buf[off] = c + (start[it] + off == gi ? deficit : 0);
+                    }
+                }
+                if (j == 0) { sh.hit_start = start[it]; sh.hit_len = len[it]; }
+            }
+        }
+        __syncthreads();
+        if (tid == 0) {
+            // A valid CDF always contains the target; the guard keeps a
+            // corrupt stream from reading unset LDS.
+            const bool hit = Lstar >= 0;
+            const int s0 = hit ? sh.hit_start : V - 1, n = hit ? sh.hit_len : 0;
+            uint32_t run = hit ? sh.hit_prefix : (1u << prec) - 1u;
+            int s = hit ? s0 + n - 1 : V - 1;
+            uint32_t clo = run, chi = hit ? run : (1u << prec);
+            for (int i = 0; i < n; i++) {
+                const uint32_t c = (uint32_t)sh.leaf_buf[i];
+                if (target < run + c) { s = s0 + i; clo = run; chi = run + c; break; }
+                run += c;
+            }
+            kr_rc_state st = D.states[row];
+            kr_bit_source src;
+            const uint32_t o = D.base ? (uint32_t)D.base[row] : 0u;
+            uint32_t lim = D.in_len > o ? D.in_len - o : 0u;
+            if (D.limits && (uint32_t)D.limits[row] < lim) lim = (uint32_t)D.limits[row];
+            src.buf = D.in + (o < D.in_len ? o : 0u);
+            src.limit = lim;
+            src.pos = st.bit_offset;
+            kr_rc_consume(st.low, st.high, st.pending_or_value, clo, chi, prec, src);
+            st.bit_offset = src.pos;
+            D.states[row] = st;
+            D.out_syms[row] = s;
+            if (D.tokens) {
+                const int cnt = D.tok_count ? D.tok_count[row] : 0;
+                if (cnt >= 0 && cnt < D.tok_stride)
+                    D.tokens[(size_t)row * (size_t)D.tok_stride + cnt] = s;
+                if (D.tok_count) D.tok_count[row] = cnt + 1;
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Host: summation plans per (device, V)
+// ---------------------------------------------------------------------------
+struct DevPlan {
+    PlanArgs args;
+    void* mem;
+};
+
+std::mutex g_plan_mu;
+std::map<std::pair<int, int>, DevPlan> g_plans;
+
+struct BuildNode { bool leaf; int id; };
+
+int build_plan(int V, std::vector<int2>& leaves, std::vector<int2>& inner_out,
+               std::vector<int>& level_start, std::vector<int>& roots) {
+    struct Inner { BuildNode l, r; int height; };
+    std::vector<Inner> inner;
+    std::vector<int> leaf_height;
+    // recursive split, numpy pairwise rule
+    struct Rec {
+        std::vector<int2>& leaves;
+        std::vector<Inner>& inner;
+        std::pair<BuildNode, int> go(int start, int n) {
+            if (n <= 128) {
+                leaves.push_back(make_int2(start, n));
+                return {BuildNode{true, (int)leaves.size() - 1}, 0};
+            }
+            int half = n / 2;
+            half -= half % 8;
+            auto l = go(start, half);
+            auto r = go(start + half, n - half);
+            const int h = 1 + std::max(l.second, r.second);
+            inner.push_back(Inner{l.first, r.first, h});
+            return {BuildNode{false, (int)inner.size() - 1}, h};
+        }
+    } rec{leaves, inner};
+    std::vector<BuildNode> block_roots;
+    for (int s = 0; s < V; s += 8192) block_roots.push_back(rec.go(s, std::min(8192, V - s)).first);
+    const int NL = (int)leaves.size(), NI = (int)inner.size();
+    // order inner nodes by height (children always have smaller height)
+    std::vector<int> order(NI);
+    for (int i = 0; i < NI; i++) order[i] = i;
+    std::stable_sort(order.begin(), order.end(),
+                     [&](int a, int b) { return inner[a].height < inner[b].height; });
+    std::vector<int> pos(NI);
+    for (int i = 0; i < NI; i++) pos[order[i]] = i;
+    auto ident = [&](BuildNode n) { return n.leaf ? n.id : NL + pos[n.id]; };
+    inner_out.resize(NI);
+    int max_h = 0;
+    for (int i = 0; i < NI; i++) {
+        const Inner& in = inner[order[i]];
+        inner_out[i] = make_int2(ident(in.l), ident(in.r));
+        max_h = std::max(max_h, in.height);
+    }
+    level_start.assign(max_h + 1, 0);
+    {
+        int idx = 0;
+        for (int h = 1; h <= max_h; h++) {
+            level_start[h - 1] = idx;
+            while (idx < NI && inner[order[idx]].height == h) idx++;
+        }
+        level_start[max_h] = idx;
+    }
+    for (auto& r : block_roots) roots.push_back(ident(r));
+    return max_h;
+}
+
+int get_plan(int V, PlanArgs* out) {
+    int dev = 0;
+    KR_HIP(hipGetDevice(&dev));
+    std::lock_guard<std::mutex> lock(g_plan_mu);
+    auto it = g_plans.find({dev, V});
+    if (it != g_plans.end()) { *out = it->second.args; return KR_OK; }
+    std::vector<int2> leaves, inner;
+    std::vector<int> level_start, roots;
+    const int n_levels = build_plan(V, leaves, inner, level_start, roots);
+    if ((int)leaves.size() > kMaxLeaves)
+        return kr_fail(KR_EUNSUPPORTED, "vocabulary %d too large (max 65536)", V);
+    const size_t nb = sizeof(int2) * (leaves.size() + inner.size()) +
+                      sizeof(int) * (level_start.size() + roots.size());
+    std::vector<char> host(nb);
+    char* p = host.data();
+    auto put = [&](const void* src, size_t bytes) { std::memcpy(p, src, bytes); p += bytes; };
+    put(leaves.data(), sizeof(int2) * leaves.size());
+    put(inner.data(), sizeof(int2) * inner.size());
+    put(level_start.data(), sizeof(int) * level_start.size());
+    put(roots.data(), sizeof(int) * roots.size());
+    void* mem = nullptr;
+    KR_HIP(hipMalloc(&mem, nb));
+    KR_HIP(hipMemcpy(mem, host.data(), nb, hipMemcpyHostToDevice));
+    char* d = static_cast<char*>(mem);
+    PlanArgs a;
+    a.leaves = reinterpret_cast<const int2*>(d);
+    d += sizeof(int2) * leaves.size();
+    a.inner = reinterpret_cast<const int2*>(d);
+    d += sizeof(int2) * inner.size();
+    a.level_start = reinterpret_cast<const int*>(d);
+    d += sizeof(int) * level_start.size();
+    a.roots = reinterpret_cast<const int*>(d);
+    a.V = V;
+    a.n_leaves = (int)leaves.size();
+    a.n_inner = (int)inner.size();
+    a.n_levels = n_levels;
+    a.n_blocks = (int)roots.size();
+    g_plans[{dev, V}] = DevPlan{a, mem};
+    *out = a;
+    return KR_OK;
+}
+
+int check_common(int N, int V, int prec) {
+    KR_REQUIRE(N >= 0, "bad row count %d", N);
+    KR_REQUIRE(V >= 1 && V <= 65536, "vocabulary %d out of range [1, 65536]", V);
+    KR_REQUIRE(prec >= 1 && prec <= 30 && V < (1 << prec), "cdf_precision %d invalid for V=%d",
+               prec, V);
+    return KR_OK;
+}
+
+template <int IN, int MODE>
+int launch_rows(const void* in, long long ld, int N, int V, int prec, void* out,
+                long long out_ld, const int32_t* symbols, const DecodeArgs& D, void* stream) {
+    int rc = check_common(N, V, prec);
+    if (rc) return rc;
+    if (N == 0) return KR_OK;
+    PlanArgs P;
+    rc = get_plan(V, &P);
+    if (rc) return rc;
+    row_cdf_kernel<IN, MODE><<<N, kThreads, 0, kr_stream(stream)>>>(in, ld, N, P, prec, out,
+                                                                     out_ld, symbols, D);
+    KR_LAUNCHED();
+    return KR_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int kr_probs_to_cdf(const float* probs, int N, int V, long long ld, uint32_t* cdf_out,
+                    int cdf_precision, void* stream) {
+    KR_REQUIRE(probs && cdf_out, "kr_probs_to_cdf: null pointer");
+    KR_REQUIRE(ld >= V, "kr_probs_to_cdf: ld %lld < V %d", ld, V);
+    return launch_rows<IN_PROBS_F32, M_CDF>(probs, ld, N, V, cdf_precision, cdf_out, V + 1,
+                                            nullptr, DecodeArgs{}, stream);
+}
+
+int kr_softmax_cdf(const uint16_t* logits, int N, int V, long long ld, int32_t* out,
+                   int cumulative, int cdf_precision, void* stream) {
+    KR_REQUIRE(logits && out, "kr_softmax_cdf: null pointer");
+    KR_REQUIRE(ld >= V, "kr_softmax_cdf: ld %lld < V %d", ld, V);
+    if (cumulative)
+        return launch_rows<IN_LOGITS_F16, M_CDF>(logits, ld, N, V, cdf_precision, out, V + 1,
+                                                 nullptr, DecodeArgs{}, stream);
+    return launch_rows<IN_LOGITS_F16, M_COUNTS>(logits, ld, N, V, cdf_precision, out, V + 1,
+                                                nullptr, DecodeArgs{}, stream);
+}
+
+int kr_softmax_probs(const uint16_t* logits, int N, int V, long long ld, float* probs,
+                     void* stream) {
+    KR_REQUIRE(logits && probs, "kr_softmax_probs: null pointer");
+    KR_REQUIRE(ld >= V, "kr_softmax_probs: ld %lld < V %d", ld, V);
+    return launch_rows<IN_LOGITS_F16, M_PROBS>(logits, ld, N, V, KR_CDF_PRECISION_DEFAULT, probs,
+                                               V, nullptr, DecodeArgs{}, stream);
+}
+
+int kr_softmax_cdf_pairs(const uint16_t* logits, int N, int V, long long ld,
+                         const int32_t* symbols, uint32_t* pairs, int cdf_precision,
+                         void* stream) {
+    KR_REQUIRE(logits && symbols && pairs, "kr_softmax_cdf_pairs: null pointer");
+    KR_REQUIRE(ld >= V, "kr_softmax_cdf_pairs: ld %lld < V %d", ld, V);
+    return launch_rows<IN_LOGITS_F16, M_PAIRS>(logits, ld, N, V, cdf_precision, pairs, 2,
+                                               symbols, DecodeArgs{}, stream);
+}
+
+int kr_softmax_cdf_decode(const uint16_t* logits, int B, int V, long long ld,
+                          const uint8_t* input_buf, uint32_t in_len,
+                          const int32_t* base_byte_offsets, const int32_t* byte_limits,
+                          uint32_t* states, int32_t* out_syms, int32_t* tokens,
+                          long long tok_stride, int32_t* tok_count, const int32_t* n_tokens,
+                          int cdf_precision, void* stream) {
+    KR_REQUIRE(logits && input_buf && states && out_syms, "kr_softmax_cdf_decode: null pointer");
+    KR_REQUIRE(ld >= V, "kr_softmax_cdf_decode: ld %lld < V %d", ld, V);
+    KR_REQUIRE(!tokens || tok_stride >= 1, "kr_softmax_cdf_decode: bad tok_stride");
+    DecodeArgs D;
+    D.in = input_buf;
+    D.in_len = in_len;
+    D.base = base_byte_offsets;
+    D.limits = byte_limits;
+    D.states = reinterpret_cast<kr_rc_state*>(states);
+    D.out_syms = out_syms;
+    D.tokens = tokens;
+    D.tok_stride = tok_stride;
+    D.tok_count = tok_count;
+    D.n_tokens = n_tokens;
+    return launch_rows<IN_LOGITS_F16, M_DECODE>(logits, ld, B, V, cdf_precision, nullptr, 0,
+                                                nullptr, D, stream);
+}
+
+}  // extern "C"

@@ -1,0 +1,229 @@
+// Model-level entry points: packed compress windows and stepped, fused
+// decode steps (optionally replayed from one captured HIP graph), plus the
+// error/introspection calls of the C ABI.
+//
+// Compress follows InferenceEngine._compress_chunk_cpp (krunch/inference.py:
+// 293-361) generalised to B chunks per call (the layer op accepts [B,T,C],
+// layer_cpp.cpp:469-474): embed -> layers -> per row block (head GEMM ->
+// softmax/CDF -> symbol interval). Decompress follows
+// _decompress_chunks_batched_cpp (inference.py:363-443): per step embed the
+// previous symbols -> layers (T = 1) -> head -> fused CDF search + range
+// decode; decoded symbols never leave the GPU.
+#include <stdarg.h>
+#include <stdio.h>
+#include <string>
+
+#include "kr_model.h"
+
+int kr_impl_forward_layers(const kr_model_weights* m, void* x, int B, int T, void* state,
+                           void* ws, size_t ws_bytes, hipStream_t s);
+int kr_impl_embed(const kr_model_weights* m, const int32_t* ids, int M, void* x, hipStream_t s);
+int kr_impl_head(const kr_model_weights* m, const void* x, int M, void* xn, void* logits,
+                 long long ld, hipStream_t s);
+size_t kr_impl_work_bytes(long long M, int C, int F);
+void* kr_impl_head_scratch(void* ws, long long M, int C, int F);
+
+extern "C" {
+int kr_softmax_cdf_pairs(const uint16_t* logits, int N, int V, long long ld,
+                         const int32_t* symbols, uint32_t* pairs, int cdf_precision,
+                         void* stream);
+int kr_softmax_cdf_decode(const uint16_t* logits, int B, int V, long long ld,
+                          const uint8_t* input_buf, uint32_t in_len,
+                          const int32_t* base_byte_offsets, const int32_t* byte_limits,
+                          uint32_t* states, int32_t* out_syms, int32_t* tokens,
+                          long long tok_stride, int32_t* tok_count, const int32_t* n_tokens,
+                          int cdf_precision, void* stream);
+int kr_probs_to_cdf(const float* probs, int N, int V, long long ld, uint32_t* cdf_out,
+                    int cdf_precision, void* stream);
+}
+
+namespace {
+thread_local std::string g_err;
+}
+
+int kr_fail(int code, const char* fmt, ...) {
+    char buf[1024];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_err = buf;
+    return code;
+}
+
+#define KR_TRY(expr)              \
+    do {                          \
+        int kr_rc_ = (expr);      \
+        if (kr_rc_) return kr_rc_; \
+    } while (0)
+
+namespace {
+
+struct DecodeStepArgs {
+    const kr_model_weights* m;
+    int B;
+    void* state;
+    int32_t* syms;
+    void* x;
+    void* ws;
+    size_t ws_bytes;
+    void* logits;
+    long long ld;
+    const uint8_t* in;
+    uint32_t in_len;
+    const int32_t* base;
+    const int32_t* limits;
+    uint32_t* ac_states;
+    int32_t* tokens;
+    long long tok_stride;
+    int32_t* tok_count;
+    const int32_t* n_tokens;
+    int prec;
+};
+
+int decode_step(const DecodeStepArgs& a, hipStream_t s) {
+    KR_TRY(kr_impl_embed(a.m, a.syms, a.B, a.x, s));
+    KR_TRY(kr_impl_forward_layers(a.m, a.x, a.B, 1, a.state, a.ws, a.ws_bytes, s));
+    void* xn = kr_impl_head_scratch(a.ws, a.B, a.m->C, a.m->F);
+    KR_TRY(kr_impl_head(a.m, a.x, a.B, xn, a.logits, a.ld, s));
+    return kr_softmax_cdf_decode(reinterpret_cast<const uint16_t*>(a.logits), a.B, a.m->V, a.ld,
+                                 a.in, a.in_len, a.base, a.limits, a.ac_states, a.syms, a.tokens,
+                                 a.tok_stride, a.tok_count, a.n_tokens, a.prec, s);
+}
+
+int check_decode(const DecodeStepArgs& a) {
+    KR_REQUIRE(a.m && a.state && a.syms && a.x && a.ws && a.logits && a.in && a.ac_states,
+               "decode: null pointer");
+    KR_REQUIRE(a.B >= 1, "decode: bad B=%d", a.B);
+    KR_REQUIRE(a.ld >= a.m->V, "decode: logits ld %lld < V %d", a.ld, a.m->V);
+    KR_REQUIRE(a.ws_bytes >= kr_impl_work_bytes(a.B, a.m->C, a.m->F), "decode: workspace too small");
+    KR_REQUIRE(!a.tokens || a.tok_count, "decode: tokens need tok_count");
+    return KR_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* kr_last_error(void) { return g_err.c_str(); }
+
+int kr_abi_version(void) { return 1; }
+
+size_t kr_forward_workspace_bytes(long long M, int C, int F) {
+    return kr_impl_work_bytes(M, C, F);
+}
+
+int kr_forward_layers(const kr_model_weights* m, void* x, int B, int T, void* state, void* ws,
+                      size_t ws_bytes, void* stream) {
+    return kr_impl_forward_layers(m, x, B, T, state, ws, ws_bytes, kr_stream(stream));
+}
+
+int kr_embed(const kr_model_weights* m, const int32_t* ids, int M, void* x, void* stream) {
+    KR_REQUIRE(m && ids && x && M >= 0, "kr_embed: bad args");
+    return kr_impl_embed(m, ids, M, x, kr_stream(stream));
+}
+
+int kr_head_logits(const kr_model_weights* m, const void* x, int M, void* xn, void* logits,
+                   long long ld, void* stream) {
+    KR_REQUIRE(m && x && xn && logits && M >= 0 && ld >= m->V, "kr_head_logits: bad args");
+    return kr_impl_head(m, x, M, xn, logits, ld, kr_stream(stream));
+}
+
+int kr_compress_window(const kr_model_weights* m, const int32_t* inputs, const int32_t* targets,
+                       int B, int T, void* state, void* x, void* ws, size_t ws_bytes,
+                       void* logits, long long ld, int head_rows, uint32_t* pairs,
+                       int cdf_precision, void* stream) {
+    KR_REQUIRE(m && inputs && targets && state && x && ws && logits && pairs,
+               "kr_compress_window: null pointer");
+    KR_REQUIRE(B >= 1 && T >= 1 && head_rows >= 1 && ld >= m->V, "kr_compress_window: bad shape");
+    const long long M = (long long)B * T;
+    KR_REQUIRE(ws_bytes >= kr_impl_work_bytes(M, m->C, m->F), "kr_compress_window: workspace too small");
+    hipStream_t s = kr_stream(stream);
+    KR_TRY(kr_impl_embed(m, inputs, (int)M, x, s));
+    KR_TRY(kr_impl_forward_layers(m, x, B, T, state, ws, ws_bytes, s));
+    void* xn = kr_impl_head_scratch(ws, M, m->C, m->F);
+    for (long long r0 = 0; r0 < M; r0 += head_rows) {
+        const int n = (int)((M - r0) < head_rows ? (M - r0) : head_rows);
+        const void* xr = static_cast<const char*>(x) + (size_t)r0 * m->C * 2;
+        void* xnr = static_cast<char*>(xn) + (size_t)r0 * m->C * 2;
+        KR_TRY(kr_impl_head(m, xr, n, xnr, logits, ld, s));
+        KR_TRY(kr_softmax_cdf_pairs(reinterpret_cast<const uint16_t*>(logits), n, m->V, ld,
+                                    targets + r0, pairs + 2 * r0, cdf_precision, stream));
+    }
+    return KR_OK;
+}
+
+int kr_decode_step(const kr_model_weights* m, int B, void* state, int32_t* syms, void* x,
+                   void* ws, size_t ws_bytes, void* logits, long long ld, const uint8_t* input_buf,
+                   uint32_t in_len, const int32_t* base_byte_offsets, const int32_t* byte_limits,
+                   uint32_t* ac_states, int32_t* tokens, long long tok_stride, int32_t* tok_count,
+                   const int32_t* n_tokens, int cdf_precision, void* stream) {
+    DecodeStepArgs a{m, B, state, syms, x, ws, ws_bytes, logits, ld, input_buf, in_len,
+                     base_byte_offsets, byte_limits, ac_states, tokens, tok_stride, tok_count,
+                     n_tokens, cdf_precision};
+    KR_TRY(check_decode(a));
+    return decode_step(a, kr_stream(stream));
+}
+
+int kr_decode_run(const kr_model_weights* m, int B, void* state, int32_t* syms, void* x,
+                  void* ws, size_t ws_bytes, void* logits, long long ld, const uint8_t* input_buf,
+                  uint32_t in_len, const int32_t* base_byte_offsets, const int32_t* byte_limits,
+                  uint32_t* ac_states, int32_t* tokens, long long tok_stride, int32_t* tok_count,
+                  const int32_t* n_tokens, int cdf_precision, int n_steps, int use_graph,
+                  void* stream) {
+    DecodeStepArgs a{m, B, state, syms, x, ws, ws_bytes, logits, ld, input_buf, in_len,
+                     base_byte_offsets, byte_limits, ac_states, tokens, tok_stride, tok_count,
+                     n_tokens, cdf_precision};
+    KR_TRY(check_decode(a));
+    KR_REQUIRE(n_steps >= 0, "kr_decode_run: bad n_steps");
+    hipStream_t s = kr_stream(stream);
+    if (n_steps == 0) return KR_OK;
+    if (!use_graph) {
+        for (int i = 0; i < n_steps; i++) KR_TRY(decode_step(a, s));
+        return KR_OK;
+    }
+    // Warm per-V caches (CDF summation plan) outside the capture: a
+    // zero-row launch builds the plan without running a kernel.
+    KR_TRY(kr_probs_to_cdf(reinterpret_cast<const float*>(logits), 0, m->V, m->V, ac_states,
+                           cdf_precision, stream));
+    hipStream_t cap = nullptr;
+    hipEvent_t ev_in = nullptr, ev_out = nullptr;
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+    int rc = KR_OK;
+    auto cleanup = [&]() {
+        if (exec) (void)hipGraphExecDestroy(exec);
+        if (graph) (void)hipGraphDestroy(graph);
+        if (ev_in) (void)hipEventDestroy(ev_in);
+        if (ev_out) (void)hipEventDestroy(ev_out);
+        if (cap) (void)hipStreamDestroy(cap);
+    };
+    auto hip_fail = [&](hipError_t e, const char* what) {
+        rc = kr_fail(KR_EHIP, "kr_decode_run: %s: %s", what, hipGetErrorString(e));
+        cleanup();
+        return rc;
+    };
+    hipError_t e;
+    if ((e = hipStreamCreateWithFlags(&cap, hipStreamNonBlocking)) != hipSuccess) return hip_fail(e, "stream");
+    if ((e = hipEventCreateWithFlags(&ev_in, hipEventDisableTiming)) != hipSuccess) return hip_fail(e, "event");
+    if ((e = hipEventCreateWithFlags(&ev_out, hipEventDisableTiming)) != hipSuccess) return hip_fail(e, "event");
+    if ((e = hipEventRecord(ev_in, s)) != hipSuccess) return hip_fail(e, "record");
+    if ((e = hipStreamWaitEvent(cap, ev_in, 0)) != hipSuccess) return hip_fail(e, "wait");
+    if ((e = hipStreamBeginCapture(cap, hipStreamCaptureModeThreadLocal)) != hipSuccess)
+        return hip_fail(e, "begin capture");
+    rc = decode_step(a, cap);
+    e = hipStreamEndCapture(cap, &graph);
+    if (rc) { cleanup(); return rc; }
+    if (e != hipSuccess) return hip_fail(e, "end capture");
+    if ((e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0)) != hipSuccess)
+        return hip_fail(e, "instantiate");
+    for (int i = 0; i < n_steps; i++)
+        if ((e = hipGraphLaunch(exec, cap)) != hipSuccess) return hip_fail(e, "graph launch");
+    if ((e = hipEventRecord(ev_out, cap)) != hipSuccess) return hip_fail(e, "record");
+    if ((e = hipStreamWaitEvent(s, ev_out, 0)) != hipSuccess) return hip_fail(e, "wait");
+    if ((e = hipStreamSynchronize(cap)) != hipSuccess) return hip_fail(e, "sync");
+    cleanup();
+    return KR_OK;
+}
+
+}  // extern "C"

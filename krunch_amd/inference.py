@@ -1,0 +1,224 @@
+"""Drop-in for the codec engine of `krunch.inference` (`krunch/inference.py`).
+
+Kept from the reference: the blob header (`encode_header`/`decode_header`,
+format ">4sBIIIHHQII", 37 bytes; inference.py:47-83), BOS = 0, the per-chunk
+mini-header ">II" (orig_len, n_tokens) followed by the range-coded bits
+(inference.py:357-360), and the engine methods `load`, `compress_chunk`,
+`decompress_chunk`, `compress_chunks_batched`, `decompress_chunks_batched`.
+
+The hot path is token level: `compress_tokens_batched` runs B chunks through
+packed windows of KRUNCH_FORWARD_BATCH (1024) tokens with RNN and coder state
+carried across windows (inference.py:311-338, generalised from one chunk to B
+chunks per call); `decompress_tokens_batched` decodes B chunks in lockstep,
+one token per stream per step, with the CDF search and range decode fused on
+the GPU and the whole step replayed from one HIP graph (inference.py:363-443).
+Byte-level methods tokenize with a `tokenizers` JSON when one is loaded.
+"""
+from __future__ import annotations
+
+import os
+import struct
+from typing import List, Optional, Sequence
+
+import numpy as np
+import torch
+
+from krunch_amd import _lib, cpp_path
+from krunch_amd.model import State
+
+BLOB_MAGIC = b"KRNC"
+BLOB_VERSION = 1
+MODEL_ID = 1
+TOKENIZER_ID = 1
+HEADER_FMT = ">4sBIIIHHQII"
+HEADER_SIZE = struct.calcsize(HEADER_FMT)
+BOS_TOKEN = 0
+CDF_PRECISION = 24
+
+
+def encode_header(original_len: int, n_chunks: int, crc32: int, adapter_id: int = 0,
+                  adapter_version: int = 0, flags: int = 0, model_id: int = MODEL_ID) -> bytes:
+    return struct.pack(HEADER_FMT, BLOB_MAGIC, BLOB_VERSION, model_id, TOKENIZER_ID, adapter_id,
+                       adapter_version, flags, original_len, n_chunks, crc32)
+
+
+def decode_header(data: bytes) -> dict:
+    if len(data) < HEADER_SIZE:
+        raise ValueError(f"blob too short: {len(data)} < {HEADER_SIZE}")
+    magic, bv, mid, tid, aid, av, flags, orig_len, n_chunks, crc = struct.unpack(
+        HEADER_FMT, data[:HEADER_SIZE])
+    if magic != BLOB_MAGIC:
+        raise ValueError(f"bad magic: {magic!r}")
+    return {"blob_version": bv, "model_id": mid, "tokenizer_id": tid, "adapter_id": aid,
+            "adapter_version": av, "flags": flags, "original_len": orig_len,
+            "n_chunks": n_chunks, "crc32": crc}
+
+
+class InferenceEngine:
+    def __init__(self):
+        self._weights = None
+        self._tokenizer = None
+        self._ready = False
+        self.window = int(os.environ.get("KRUNCH_FORWARD_BATCH", "1024"))
+        self.use_graph = os.environ.get("KRUNCH_HIP_GRAPH", "1") == "1"
+
+    # ------------------------------------------------------------------ setup
+    def load(self, weights: Optional[dict] = None, tokenizer_path: Optional[str] = None,
+             device: str = "cuda"):
+        """Prepare weights (a dict in the rwkv-package layout; default: the
+        synthetic RWKV-4-169M-shaped model, seed 0) and an optional tokenizer."""
+        if weights is None:
+            from krunch_amd.synthetic import make_weights
+            weights = make_weights()
+        self._weights = cpp_path.init_weights(weights, device)
+        if tokenizer_path:
+            from tokenizers import Tokenizer
+            self._tokenizer = Tokenizer.from_file(str(tokenizer_path))
+        self._ready = True
+        return self
+
+    @property
+    def ready(self) -> bool:
+        return self._ready
+
+    @property
+    def weights(self):
+        return self._weights
+
+    # -------------------------------------------------------------- compress
+    def compress_tokens_batched(self, token_streams: Sequence[np.ndarray],
+                                orig_lens: Optional[Sequence[int]] = None) -> List[bytes]:
+        """B token streams -> B chunk payloads (">II" mini-header + bits)."""
+        assert self._ready, "call load() first"
+        W = self._weights
+        P = W["prepared"]
+        dev = P.device
+        B = len(token_streams)
+        if B == 0:
+            return []
+        lens = np.array([len(t) for t in token_streams], dtype=np.int64)
+        if (lens < 1).any():
+            raise ValueError("chunk has no tokens")
+        Tmax = int(lens.max())
+        tok = np.zeros((B, Tmax), dtype=np.int32)
+        for b, t in enumerate(token_streams):
+            tok[b, :len(t)] = np.asarray(t, dtype=np.int32)
+        if tok.min() < 0 or tok.max() >= P.V:
+            raise ValueError(f"token id out of range [0, {P.V})")
+        inp = np.zeros_like(tok)
+        inp[:, 0] = BOS_TOKEN
+        inp[:, 1:] = tok[:, :-1]
+        tok_d = torch.from_numpy(tok).to(dev)
+        inp_d = torch.from_numpy(inp).to(dev)
+
+        per_cap = int(4 * Tmax + 64)
+        out = torch.zeros(B * per_cap, dtype=torch.uint8, device=dev)
+        base = torch.arange(B, dtype=torch.int32, device=dev) * per_cap
+        ac = torch.zeros((B, 4), dtype=torch.int64)
+        ac[:, 1] = 0xFFFFFFFF
+        ac = ac.to(torch.uint32).to(dev).contiguous()
+        err = torch.zeros(1, dtype=torch.uint32, device=dev)
+        state = State(P.n_layer, B, P.C, dev)
+        Tw = min(self.window, Tmax)
+        M = B * Tw
+        ws, nbytes = cpp_path.workspace(W, M)
+        x = torch.empty((M, P.C), dtype=torch.float16, device=dev)
+        head_rows = min(M, 2048)
+        logits = torch.empty((head_rows, P.V), dtype=torch.float16, device=dev)
+        pairs = torch.empty((M, 2), dtype=torch.uint32, device=dev)
+        lens_d = torch.from_numpy(lens.astype(np.int32)).to(dev)
+        s = _lib.stream_ptr()
+        for w0 in range(0, Tmax, Tw):
+            T = min(Tw, Tmax - w0)
+            ids = inp_d[:, w0:w0 + T].contiguous()
+            tgt = tok_d[:, w0:w0 + T].contiguous()
+            _lib.call("kr_compress_window", P.ptr, ids.data_ptr(), tgt.data_ptr(), B, T, state.ptr,
+                      x.data_ptr(), ws.data_ptr(), nbytes, logits.data_ptr(), P.V, head_rows,
+                      pairs.data_ptr(), CDF_PRECISION, s)
+            n_valid = (lens_d - w0).clamp(0, T).to(torch.int32).contiguous()
+            _lib.call("kr_encode_pairs_batched", pairs.data_ptr(), T, T, n_valid.data_ptr(),
+                      out.data_ptr(), out.numel(), base.data_ptr(), ac.data_ptr(), B,
+                      CDF_PRECISION, err.data_ptr(), s)
+        _lib.call("kr_encode_finalize_batched", out.data_ptr(), out.numel(), base.data_ptr(),
+                  ac.data_ptr(), B, err.data_ptr(), s)
+        if int(err.item()):
+            raise RuntimeError("range coder output buffer overflow")
+        bits = ac[:, 3].to(torch.int64).cpu().numpy()
+        host = out.cpu().numpy()
+        res = []
+        for b in range(B):
+            n = int((bits[b] + 7) // 8)
+            ol = int(orig_lens[b]) if orig_lens is not None else 4 * int(lens[b])
+            res.append(struct.pack(">II", ol, int(lens[b])) +
+                       host[b * per_cap:b * per_cap + n].tobytes())
+        return res
+
+    # ------------------------------------------------------------ decompress
+    def decompress_tokens_batched(self, encoded_chunks: Sequence[bytes]) -> List[np.ndarray]:
+        """Chunk payloads -> token streams, B streams decoded in lockstep."""
+        assert self._ready, "call load() first"
+        W = self._weights
+        P = W["prepared"]
+        dev = P.device
+        B = len(encoded_chunks)
+        if B == 0:
+            return []
+        n_tok, streams = [], []
+        for enc in encoded_chunks:
+            _, nt = struct.unpack(">II", enc[:8])
+            n_tok.append(nt)
+            streams.append(enc[8:])
+        offs = np.cumsum([0] + [len(s) for s in streams])
+        cat = np.frombuffer(b"".join(streams) + b"\0", dtype=np.uint8)
+        inbuf = torch.from_numpy(cat.copy()).to(dev)
+        base = torch.from_numpy(offs[:-1].astype(np.int32)).to(dev)
+        limits = torch.from_numpy(np.array([len(s) for s in streams], dtype=np.int32)).to(dev)
+        ac = torch.empty((B, 4), dtype=torch.uint32, device=dev)
+        s = _lib.stream_ptr()
+        _lib.call("kr_decode_init_batched", inbuf.data_ptr(), inbuf.numel(), base.data_ptr(),
+                  limits.data_ptr(), ac.data_ptr(), B, s)
+        Tmax = max(n_tok)
+        state = State(P.n_layer, B, P.C, dev)
+        syms = torch.full((B,), BOS_TOKEN, dtype=torch.int32, device=dev)
+        tokens = torch.zeros((B, Tmax), dtype=torch.int32, device=dev)
+        count = torch.zeros(B, dtype=torch.int32, device=dev)
+        ntd = torch.tensor(n_tok, dtype=torch.int32, device=dev)
+        x = torch.empty((B, P.C), dtype=torch.float16, device=dev)
+        ws, nbytes = cpp_path.workspace(W, B)
+        logits = torch.empty((B, P.V), dtype=torch.float16, device=dev)
+        _lib.call("kr_decode_run", P.ptr, B, state.ptr, syms.data_ptr(), x.data_ptr(),
+                  ws.data_ptr(), nbytes, logits.data_ptr(), P.V, inbuf.data_ptr(), inbuf.numel(),
+                  base.data_ptr(), limits.data_ptr(), ac.data_ptr(), tokens.data_ptr(), Tmax,
+                  count.data_ptr(), ntd.data_ptr(), CDF_PRECISION, Tmax,
+                  1 if self.use_graph else 0, s)
+        host = tokens.cpu().numpy()
+        return [host[b, :n_tok[b]].copy() for b in range(B)]
+
+    # ------------------------------------------------------------ byte level
+    def _need_tokenizer(self):
+        if self._tokenizer is None:
+            raise RuntimeError("byte-level API needs a tokenizer: load(tokenizer_path=...)")
+
+    def compress_chunk(self, data: bytes) -> bytes:
+        return self.compress_chunks_batched([data])[0]
+
+    def compress_chunks_batched(self, chunks: Sequence[bytes]) -> List[bytes]:
+        self._need_tokenizer()
+        toks = [np.array(self._tokenizer.encode(c.decode("utf-8", errors="replace")).ids,
+                         dtype=np.int32) for c in chunks]
+        return self.compress_tokens_batched(toks, orig_lens=[len(c) for c in chunks])
+
+    def decompress_chunk(self, encoded: bytes) -> bytes:
+        return self.decompress_chunks_batched([encoded])[0]
+
+    def decompress_chunks_batched(self, encoded_chunks: Sequence[bytes]) -> List[bytes]:
+        self._need_tokenizer()
+        toks = self.decompress_tokens_batched(encoded_chunks)
+        out = []
+        for enc, t in zip(encoded_chunks, toks):
+            orig_len, _ = struct.unpack(">II", enc[:8])
+            out.append(self._tokenizer.decode(t.tolist()).encode("utf-8")[:orig_len])
+        return out
+
+
+engine = InferenceEngine()

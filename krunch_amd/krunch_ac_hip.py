@@ -1,0 +1,237 @@
+"""Drop-in for the reference's `krunch_ac_cuda` extension ops, on the HIP library.
+
+Same op names, argument order and in-place semantics as the pybind module
+(`krunch_ac/cuda/main.cpp:114-303,354-466`, `layer_cpp.cpp:824-1052`):
+the caller owns coder state and buffers (mutated in place, launches are
+asynchronous on the current stream); ops that produce tensors allocate them.
+Argument errors raise RuntimeError, as TORCH_CHECK does. Differences: every
+call is bounds-checked against the buffers it is given, and the CDF
+precision is taken from the CDF itself (cdf[:, -1] = 2^precision) or passed
+explicitly.
+"""
+from __future__ import annotations
+
+import weakref
+
+import torch
+
+from krunch_amd import _lib
+
+CDF_PRECISION = 24
+
+
+def _check(cond, msg):
+    if not cond:
+        raise RuntimeError(msg)
+
+
+def _cuda(t, dtype, name):
+    _check(t.is_cuda, f"{name} must be a device tensor")
+    _check(t.dtype == dtype, f"{name} must be {dtype}, got {t.dtype}")
+    _check(t.is_contiguous(), f"{name} must be contiguous")
+
+
+def _nbytes(t):
+    return t.numel() * t.element_size()
+
+
+# ---------------------------------------------------------------------------
+# range coder (encode_kernel.cu / decode_kernel.cu ops)
+# ---------------------------------------------------------------------------
+
+def encode_step(cdf, symbols, output_buf, state, precision: int = CDF_PRECISION):
+    """Encode N rows of one stream: cdf int32 [N, V+1], symbols int32 [N]."""
+    _cuda(cdf, torch.int32, "cdf"); _cuda(symbols, torch.int32, "symbols")
+    _cuda(output_buf, torch.uint8, "output_buf"); _cuda(state, torch.uint32, "state")
+    _check(cdf.dim() == 2 and symbols.numel() == cdf.shape[0], "cdf/symbols shape mismatch")
+    _check(state.numel() >= 4, "state must hold 4 uint32")
+    _lib.call("kr_encode_step", cdf.data_ptr(), cdf.shape[1], symbols.data_ptr(), cdf.shape[0],
+              output_buf.data_ptr(), _nbytes(output_buf), state.data_ptr(), precision, None,
+              _lib.stream_ptr())
+
+
+def encode_finalize(output_buf, state):
+    _cuda(output_buf, torch.uint8, "output_buf"); _cuda(state, torch.uint32, "state")
+    _lib.call("kr_encode_finalize", output_buf.data_ptr(), _nbytes(output_buf), state.data_ptr(),
+              None, _lib.stream_ptr())
+
+
+def decode_init(input_buf, state):
+    _cuda(input_buf, torch.uint8, "input_buf"); _cuda(state, torch.uint32, "state")
+    _lib.call("kr_decode_init_batched", input_buf.data_ptr(), _nbytes(input_buf), None, None,
+              state.data_ptr(), 1, _lib.stream_ptr())
+
+
+def decode_step(cdf, input_buf, state, out_sym, precision: int = CDF_PRECISION):
+    """Decode one symbol: cdf int32 [V+1]; out_sym int32 [1]."""
+    _cuda(cdf, torch.int32, "cdf"); _cuda(input_buf, torch.uint8, "input_buf")
+    _cuda(state, torch.uint32, "state"); _cuda(out_sym, torch.int32, "out_sym")
+    V = cdf.numel() - 1
+    _lib.call("kr_decode_step_batched", cdf.data_ptr(), V, input_buf.data_ptr(),
+              _nbytes(input_buf), None, None, state.data_ptr(), out_sym.data_ptr(), 1, precision,
+              _lib.stream_ptr())
+
+
+def encode_step_batched(cdfs, symbols, output_buf, base_byte_offsets, states,
+                        precision: int = CDF_PRECISION):
+    _cuda(cdfs, torch.int32, "cdfs"); _cuda(symbols, torch.int32, "symbols")
+    _cuda(output_buf, torch.uint8, "output_buf"); _cuda(base_byte_offsets, torch.int32, "offsets")
+    _cuda(states, torch.uint32, "states")
+    B = symbols.numel()
+    _check(cdfs.dim() == 2 and cdfs.shape[0] == B and base_byte_offsets.numel() == B
+           and states.numel() == 4 * B, "batched shapes mismatch")
+    _lib.call("kr_encode_step_batched", cdfs.data_ptr(), cdfs.shape[1] - 1, symbols.data_ptr(),
+              output_buf.data_ptr(), _nbytes(output_buf), base_byte_offsets.data_ptr(),
+              states.data_ptr(), B, precision, None, _lib.stream_ptr())
+
+
+def encode_finalize_batched(output_buf, base_byte_offsets, states):
+    _cuda(output_buf, torch.uint8, "output_buf"); _cuda(base_byte_offsets, torch.int32, "offsets")
+    _cuda(states, torch.uint32, "states")
+    B = base_byte_offsets.numel()
+    _check(states.numel() == 4 * B, "states must be [4*B]")
+    _lib.call("kr_encode_finalize_batched", output_buf.data_ptr(), _nbytes(output_buf),
+              base_byte_offsets.data_ptr(), states.data_ptr(), B, None, _lib.stream_ptr())
+
+
+def decode_init_batched(input_buf, base_byte_offsets, states, byte_limits=None):
+    _cuda(input_buf, torch.uint8, "input_buf"); _cuda(base_byte_offsets, torch.int32, "offsets")
+    _cuda(states, torch.uint32, "states")
+    B = base_byte_offsets.numel()
+    _check(states.numel() == 4 * B, "states must be [4*B]")
+    _lib.call("kr_decode_init_batched", input_buf.data_ptr(), _nbytes(input_buf),
+              base_byte_offsets.data_ptr(), _lib.ptr(byte_limits), states.data_ptr(), B,
+              _lib.stream_ptr())
+
+
+def decode_step_batched(cdfs, input_buf, base_byte_offsets, states, out_syms, byte_limits=None,
+                        precision: int = CDF_PRECISION):
+    _cuda(cdfs, torch.int32, "cdfs"); _cuda(input_buf, torch.uint8, "input_buf")
+    _cuda(base_byte_offsets, torch.int32, "offsets"); _cuda(states, torch.uint32, "states")
+    _cuda(out_syms, torch.int32, "out_syms")
+    B = out_syms.numel()
+    _check(cdfs.dim() == 2 and cdfs.shape[0] == B and states.numel() == 4 * B,
+           "batched shapes mismatch")
+    _lib.call("kr_decode_step_batched", cdfs.data_ptr(), cdfs.shape[1] - 1, input_buf.data_ptr(),
+              _nbytes(input_buf), base_byte_offsets.data_ptr(), _lib.ptr(byte_limits),
+              states.data_ptr(), out_syms.data_ptr(), B, precision, _lib.stream_ptr())
+
+
+# ---------------------------------------------------------------------------
+# softmax -> CDF (det_softmax_cdf.cu op)
+# ---------------------------------------------------------------------------
+
+def _precision_of(cdf_T_value: int) -> int:
+    p = int(cdf_T_value).bit_length() - 1
+    _check(p >= 1 and (1 << p) == int(cdf_T_value), "cdf_T_value must be a power of two")
+    return p
+
+
+def det_softmax_cdf(logits, cdf_T_value: int):
+    """fp16 logits [T, V] -> int32 [T, V+1]: column 0 = 0, columns 1..V the
+    per-symbol counts (deficit applied); the caller scans (cpp_path.py:490-501)."""
+    _cuda(logits, torch.float16, "logits")
+    _check(logits.dim() == 2, "logits must be [T, V]")
+    T, V = logits.shape
+    out = torch.empty((T, V + 1), dtype=torch.int32, device=logits.device)
+    _lib.call("kr_softmax_cdf", logits.data_ptr(), T, V, V, out.data_ptr(), 0,
+              _precision_of(cdf_T_value), _lib.stream_ptr())
+    return out
+
+
+def softmax_cdf(logits, cdf_T_value: int = 1 << CDF_PRECISION):
+    """fp16 logits [T, V] -> cumulative int32 CDF [T, V+1] in one kernel."""
+    _cuda(logits, torch.float16, "logits")
+    T, V = logits.shape
+    out = torch.empty((T, V + 1), dtype=torch.int32, device=logits.device)
+    _lib.call("kr_softmax_cdf", logits.data_ptr(), T, V, V, out.data_ptr(), 1,
+              _precision_of(cdf_T_value), _lib.stream_ptr())
+    return out
+
+
+def softmax_probs(logits):
+    """fp16 logits [T, V] -> float32 softmax probabilities (the CDF's input)."""
+    _cuda(logits, torch.float16, "logits")
+    T, V = logits.shape
+    out = torch.empty((T, V), dtype=torch.float32, device=logits.device)
+    _lib.call("kr_softmax_probs", logits.data_ptr(), T, V, V, out.data_ptr(), _lib.stream_ptr())
+    return out
+
+
+# ---------------------------------------------------------------------------
+# matmul / layer ops (layer_cpp.cpp)
+# ---------------------------------------------------------------------------
+
+_WT_CACHE: "weakref.WeakKeyDictionary" = weakref.WeakKeyDictionary()
+
+
+def _wt(W):
+    """Transposed copy of a [K, N] weight, cached per tensor object and version."""
+    hit = _WT_CACHE.get(W)
+    if hit is None or hit[0] != W._version:
+        K, N = W.shape
+        wt = torch.empty((N, K), dtype=torch.float16, device=W.device)
+        _lib.call("kr_transpose_f16", W.data_ptr(), N, K, N, wt.data_ptr(), K, _lib.stream_ptr())
+        hit = (W._version, wt)
+        _WT_CACHE[W] = hit
+    return hit[1]
+
+
+def det_matmul(x, W, out_dtype=None):
+    """y = x @ W, x fp16 [M, K], W fp16 [K, N]; fp32 accumulation in a fixed
+    K order, so each row's result does not depend on M."""
+    _cuda(x, torch.float16, "x"); _cuda(W, torch.float16, "W")
+    M, K = x.shape
+    _check(W.shape[0] == K, "inner dimensions differ")
+    N = W.shape[1]
+    dtype = out_dtype or torch.float16
+    out = torch.empty((M, N), dtype=dtype, device=x.device)
+    ep = 0 if dtype == torch.float32 else 1
+    _lib.call("kr_det_matmul", x.data_ptr(), M, K, _wt(W).data_ptr(), K, N, out.data_ptr(), N,
+              ep, None, None, _lib.stream_ptr())
+    return out
+
+
+def rwkv4_layer_step_cpp(x, att_xx, aa, bb, pp, ffn_xx, ln1_w, ln1_b, tm_k, tm_v, tm_r,
+                         time_decay, time_first, Kw, Vw, Rw, Ow, ln2_w, ln2_b, ffn_tm_k,
+                         ffn_tm_r, ffn_Kw, ffn_Vw, ffn_Rw):
+    """One RWKV-4 layer over x [B, T, C] fp16 (any B, T); state mutated in
+    place; returns the new x. `time_decay` is w = -exp(raw) as the reference's
+    rwkv loader passes it (wkv_kernel.cu:41-45)."""
+    _cuda(x, torch.float16, "x")
+    B, T, C = x.shape
+    F = ffn_Kw.shape[1]
+    dev = x.device
+    keep = []
+
+    def h(t):
+        t = t.to(device=dev, dtype=torch.float16).reshape(-1).contiguous()
+        keep.append(t)
+        return t.data_ptr()
+
+    def f32(t):
+        t = t.to(device=dev, dtype=torch.float32).reshape(-1).contiguous()
+        keep.append(t)
+        return t.data_ptr()
+
+    L = _lib.KrLayerWeights()
+    L.ln1_w, L.ln1_b, L.tm_k, L.tm_v, L.tm_r = map(h, (ln1_w, ln1_b, tm_k, tm_v, tm_r))
+    L.decay, L.first = f32(time_decay), f32(time_first)
+    def wt(m):
+        _cuda(m, torch.float16, "weight")
+        return _wt(m).data_ptr()
+
+    L.Kt, L.Vt, L.Rt, L.Ot = map(wt, (Kw, Vw, Rw, Ow))
+    L.ln2_w, L.ln2_b, L.ftm_k, L.ftm_r = map(h, (ln2_w, ln2_b, ffn_tm_k, ffn_tm_r))
+    L.fKt, L.fVt, L.fRt = map(wt, (ffn_Kw, ffn_Vw, ffn_Rw))
+    for t, dt, n in ((att_xx, torch.float16, "att_xx"), (aa, torch.float32, "aa"),
+                     (bb, torch.float32, "bb"), (pp, torch.float32, "pp"),
+                     (ffn_xx, torch.float16, "ffn_xx")):
+        _cuda(t, dt, n)
+    out = x.contiguous().clone()
+    ws_bytes = _lib.lib().kr_forward_workspace_bytes(B * T, C, F)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+    _lib.call("kr_layer_step", L, C, F, out.data_ptr(), B, T, att_xx.data_ptr(), aa.data_ptr(),
+              bb.data_ptr(), pp.data_ptr(), ffn_xx.data_ptr(), ws.data_ptr(), ws_bytes,
+              _lib.stream_ptr())
+    return out

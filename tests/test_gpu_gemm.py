@@ -1,0 +1,70 @@
+"""MFMA GEMM: against a float32 torch reference of the same op, every
+epilogue, and bit-identity of a row's result across M (different tile
+shapes), which the packed/stepped round trip relies on."""
+import numpy as np
+import pytest
+import torch
+
+from krunch_amd import _lib
+from krunch_amd import krunch_ac_hip as ops
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _mk(M, K, N, seed):
+    g = torch.Generator(device="cpu").manual_seed(seed)
+    x = (torch.randn(M, K, generator=g)).to(torch.float16).to(DEV)
+    W = (torch.randn(K, N, generator=g) * 0.02).to(torch.float16).to(DEV)
+    return x, W
+
+
+@pytest.mark.parametrize("M,K,N", [(1, 768, 768), (17, 768, 3072), (128, 3072, 768),
+                                   (1024, 768, 768), (5000, 768, 768), (300, 768, 50277)])
+def test_matmul_vs_fp32_reference(M, K, N):
+    x, W = _mk(M, K, N, M + N)
+    ref = x.float() @ W.float()
+    y32 = ops.det_matmul(x, W, torch.float32)
+    torch.testing.assert_close(y32, ref, rtol=1e-3, atol=1e-3)
+    y16 = ops.det_matmul(x, W)
+    torch.testing.assert_close(y16.float(), ref, rtol=2e-3, atol=2e-3)
+
+
+def test_rows_bit_identical_across_M():
+    K, N = 768, 3072
+    x, W = _mk(8192, K, N, 1)
+    full = ops.det_matmul(x, W, torch.float32)          # 128x128 tiles
+    mid = ops.det_matmul(x[:2048].contiguous(), W, torch.float32)   # 64x64 tiles
+    small = ops.det_matmul(x[:200].contiguous(), W, torch.float32)  # 32x32 tiles
+    one = ops.det_matmul(x[37:38].contiguous(), W, torch.float32)
+    assert torch.equal(full[:2048], mid)
+    assert torch.equal(full[:200], small)
+    assert torch.equal(full[37:38], one)
+
+
+def _run(ep, x, Wt, N, res=None, gate=None):
+    M, K = x.shape
+    out = torch.empty((M, N), dtype=torch.float32 if ep == 0 else torch.float16, device=DEV)
+    if res is not None:
+        out.copy_(res)
+    _lib.call("kr_det_matmul", x.data_ptr(), M, K, Wt.data_ptr(), K, N, out.data_ptr(), N, ep,
+              _lib.ptr(out if res is not None else None), _lib.ptr(gate), _lib.stream_ptr())
+    return out
+
+
+def test_epilogues():
+    M, K, N = 333, 768, 768
+    x, W = _mk(M, K, N, 5)
+    Wt = W.t().contiguous()
+    acc = ops.det_matmul(x, W, torch.float32)
+    h = acc.half().float()
+    res = torch.randn(M, N, device=DEV).half()
+    gate = torch.rand(M, N, device=DEV).half()
+    torch.testing.assert_close(_run(2, x, Wt, N).float(), torch.sigmoid(h).half().float(),
+                               rtol=0, atol=1e-3)
+    torch.testing.assert_close(_run(3, x, Wt, N).float(), (torch.relu(h) ** 2).half().float(),
+                               rtol=0, atol=1e-3)
+    torch.testing.assert_close(_run(4, x, Wt, N, res=res).float(), (res.float() + h).half().float(),
+                               rtol=0, atol=2e-3)
+    want = (res.float() + (gate.float() * h).half().float()).half().float()
+    torch.testing.assert_close(_run(5, x, Wt, N, res=res, gate=gate).float(), want, rtol=0, atol=2e-3)
