@@ -162,19 +162,20 @@ def softmax_probs(logits):
 # matmul / layer ops (layer_cpp.cpp)
 # ---------------------------------------------------------------------------
 
-_WT_CACHE: "weakref.WeakKeyDictionary" = weakref.WeakKeyDictionary()
+_WT_CACHE: dict = {}
 
 
 def _wt(W):
-    """Transposed copy of a [K, N] weight, cached per tensor object and version."""
-    hit = _WT_CACHE.get(W)
-    if hit is None or hit[0] != W._version:
+    """Transposed copy of a [K, N] weight, cached per live tensor object and version."""
+    key = id(W)
+    hit = _WT_CACHE.get(key)
+    if hit is None or hit[0]() is not W or hit[1] != W._version:
         K, N = W.shape
         wt = torch.empty((N, K), dtype=torch.float16, device=W.device)
         _lib.call("kr_transpose_f16", W.data_ptr(), N, K, N, wt.data_ptr(), K, _lib.stream_ptr())
-        hit = (W._version, wt)
-        _WT_CACHE[W] = hit
-    return hit[1]
+        hit = (weakref.ref(W, lambda _r, k=key: _WT_CACHE.pop(k, None)), W._version, wt)
+        _WT_CACHE[key] = hit
+    return hit[2]
 
 
 def det_matmul(x, W, out_dtype=None):
