@@ -1,0 +1,337 @@
+#!/usr/bin/env python3
+"""Benchmark: krunch compress & decompress throughput on one MI355X.
+
+Workload (one window per step): B = 256 chunks of
+Zipf(1.1) tokens with 5% repeated 64-token spans, RWKV-4-169M-shaped
+random-init weights in fp16. One step = one 1024-token window of every
+chunk: packed compress (12 layers over B*T = 262,144 rows, head, softmax ->
+CDF interval, range encode), then stepped decompress of the same window
+(1024 lockstep steps of B tokens, fused CDF search + range decode, replayed
+from a HIP graph). RNN and coder state carry across windows on both sides.
+Inputs are resident in HBM before the timed region; after it, every decoded
+token is checked against the input (byte-exact round trip).
+
+value = input KB/s of the round trip, KB = 1024 B at 4 B/token:
+  K*B*T*4/1024 / (t_compress + t_decompress).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+BYTES_PER_TOKEN = 4
+FLOP_PER_TOKEN = 261_250_560        # 12 x 2 x (5*768^2 + 2*768*3072) + 2*768*50277
+MI355X_FP16_PEAK = 2.5e15
+MI355X_HBM_PEAK = 8.0e12
+
+
+def parse():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=3)
+    ap.add_argument("--warmup", type=int, default=1)
+    ap.add_argument("--batch", type=int, default=256)
+    ap.add_argument("--window", type=int, default=1024)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-decode-steps", type=int, default=48)
+    ap.add_argument("--kernel-probe", action="store_true",
+                    help="only run a 256 MiB device copy (counter calibration) and 8 launches of "
+                         "the dominant kernel, for rocprofv3 --pmc runs")
+    return ap.parse_args()
+
+
+def kernel_probe(weights16, B):
+    """A plain copy of known size, then the dominant kernel, eagerly (one
+    dispatch each), so hardware counters can be read per dispatch."""
+    import torch
+    from krunch_amd import _lib, cpp_path
+
+    dev = torch.device("cuda")
+    src = torch.ones(64 << 20, dtype=torch.float32, device=dev)       # 256 MiB
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    W = cpp_path.init_weights(weights16, "cuda")
+    P = W["prepared"]
+    K, N, M = P.F, P.C, B
+    A = torch.rand((M, K), device=dev).half()
+    res = torch.randn((M, N), device=dev).half()
+    gate = torch.rand((M, N), device=dev).half()
+    out = torch.empty((M, N), dtype=torch.float16, device=dev)
+    Wt = P.tensors["0.fVt"]
+    for _ in range(8):
+        _lib.call("kr_det_matmul", A.data_ptr(), M, K, Wt.data_ptr(), K, N, out.data_ptr(), N, 5,
+                  res.data_ptr(), gate.data_ptr(), _lib.stream_ptr())
+    torch.cuda.synchronize()
+    print(json.dumps({"probe": "ok", "copy_bytes": 2 * src.numel() * 4}))
+
+
+def gpu_bench(args, weights16):
+    import numpy as np
+    import torch
+    from krunch_amd import _lib, cpp_path, synthetic
+    from krunch_amd.model import State
+
+    dev = torch.device("cuda")
+    W = cpp_path.init_weights(weights16, "cuda")
+    P = W["prepared"]
+    B, Tw = args.batch, args.window
+    n_win = args.warmup + args.steps
+    L = n_win * Tw
+    toks = synthetic.zipf_tokens(B, L, repeat_rate=0.05)
+    inp = synthetic.model_inputs(toks)
+    tok_d = torch.from_numpy(toks).to(dev)
+    inp_d = torch.from_numpy(inp).to(dev)
+    win_inp = [inp_d[:, w * Tw:(w + 1) * Tw].contiguous() for w in range(n_win)]
+    win_tok = [tok_d[:, w * Tw:(w + 1) * Tw].contiguous() for w in range(n_win)]
+    s = _lib.stream_ptr()
+    PREC = 24
+
+    # ------------------------------------------------------------- compress
+    M = B * Tw
+    ws, ws_bytes = cpp_path.workspace(W, M)
+    x = torch.empty((M, P.C), dtype=torch.float16, device=dev)
+    head_rows = min(M, 4096)
+    logits = torch.empty((head_rows, P.V), dtype=torch.float16, device=dev)
+    pairs = torch.empty((M, 2), dtype=torch.int32, device=dev)
+    cap = 4 * L + 64
+    out = torch.zeros(B * cap, dtype=torch.uint8, device=dev)
+    base = (torch.arange(B, dtype=torch.int32, device=dev) * cap).contiguous()
+    ac = torch.zeros((B, 4), dtype=torch.int64)
+    ac[:, 1] = 0xFFFFFFFF
+    ac = ac.to(torch.uint32).to(dev).contiguous()
+    err = torch.zeros(1, dtype=torch.uint32, device=dev)
+    cstate = State(P.n_layer, B, P.C, dev)
+
+    def compress_window(w):
+        _lib.call("kr_compress_window", P.ptr, win_inp[w].data_ptr(), win_tok[w].data_ptr(), B, Tw,
+                  cstate.ptr, x.data_ptr(), ws.data_ptr(), ws_bytes, logits.data_ptr(), P.V,
+                  head_rows, pairs.data_ptr(), PREC, s)
+        _lib.call("kr_encode_pairs_batched", pairs.data_ptr(), Tw, Tw, None, out.data_ptr(),
+                  out.numel(), base.data_ptr(), ac.data_ptr(), B, PREC, err.data_ptr(), s)
+
+    for w in range(args.warmup):
+        compress_window(w)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for w in range(args.warmup, n_win):
+        compress_window(w)
+    torch.cuda.synchronize()
+    t_c = time.perf_counter() - t0
+    _lib.call("kr_encode_finalize_batched", out.data_ptr(), out.numel(), base.data_ptr(),
+              ac.data_ptr(), B, err.data_ptr(), s)
+    torch.cuda.synchronize()
+    assert int(err.item()) == 0, "coder output overflow"
+    nbytes = ((ac[:, 3].to(torch.int64) + 7) // 8).to(torch.int32).contiguous()
+    comp_bytes = int(nbytes.sum().item())
+
+    # ----------------------------------------------------------- decompress
+    del ws, x, logits, pairs
+    dws, dws_bytes = cpp_path.workspace(W, B)
+    dx = torch.empty((B, P.C), dtype=torch.float16, device=dev)
+    dlogits = torch.empty((B, P.V), dtype=torch.float16, device=dev)
+    dac = torch.empty((B, 4), dtype=torch.uint32, device=dev)
+    _lib.call("kr_decode_init_batched", out.data_ptr(), out.numel(), base.data_ptr(),
+              nbytes.data_ptr(), dac.data_ptr(), B, s)
+    dstate = State(P.n_layer, B, P.C, dev)
+    syms = torch.zeros(B, dtype=torch.int32, device=dev)
+    dtoks = torch.zeros((B, L), dtype=torch.int32, device=dev)
+    cnt = torch.zeros(B, dtype=torch.int32, device=dev)
+
+    def decode(n_steps):
+        _lib.call("kr_decode_run", P.ptr, B, dstate.ptr, syms.data_ptr(), dx.data_ptr(),
+                  dws.data_ptr(), dws_bytes, dlogits.data_ptr(), P.V, out.data_ptr(), out.numel(),
+                  base.data_ptr(), nbytes.data_ptr(), dac.data_ptr(), dtoks.data_ptr(), L,
+                  cnt.data_ptr(), None, PREC, n_steps, 1, s)
+
+    if args.warmup:
+        decode(args.warmup * Tw)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    decode(args.steps * Tw)
+    torch.cuda.synchronize()
+    t_d = time.perf_counter() - t0
+    exact = bool(torch.equal(dtoks, tok_d))
+    if not exact:
+        bad = (dtoks != tok_d).nonzero()
+        raise SystemExit(f"round trip NOT byte-exact; first mismatch (stream, token) = {bad[0].tolist()}")
+    ntok = args.steps * B * Tw
+    return dict(t_c=t_c, t_d=t_d, ntok=ntok, comp_bytes=comp_bytes, total_tok=B * L, exact=exact)
+
+
+def dominant_kernel_roofline(weights16, B):
+    """Live roofline of the dominant kernel of the timed region: the stepped
+    channel-mix value GEMM (M = B rows, K = 3072, N = 768, gated-residual
+    epilogue; the small-M MFMA kernel), 12 launches per decode step.
+
+    It is HBM-bound: algorithmic bytes per launch = W (K*N*2) + A (M*K*2) +
+    residual, gate and output (3*M*N*2). The average launch duration is
+    measured with HIP events on the launching stream around a captured graph
+    of back-to-back launches (graph replay keeps host launch cost out). As in
+    a decode step, where the other 256 MB of weights stream between two uses
+    of one layer's matrix, every launch reads a different weight copy (64
+    copies, 302 MB > the 256 MB Infinity Cache), so W comes from HBM.
+    `traffic` is read from the committed counter summary
+    profiles/gemm_skinny_ffn_value_B256_traffic.json (rocprofv3 --pmc
+    FETCH_SIZE / WRITE_SIZE, scaled by a 256 MiB copy calibration)."""
+    import torch
+    from krunch_amd import _lib, cpp_path
+
+    W = cpp_path.init_weights(weights16, "cuda")
+    P = W["prepared"]
+    K, N, M = P.F, P.C, B
+    dev = torch.device("cuda")
+    g = torch.Generator(device="cpu").manual_seed(3)
+    A = torch.rand((M, K), generator=g).half().to(dev)
+    res = torch.randn((M, N), generator=g).half().to(dev)
+    gate = torch.rand((M, N), generator=g).half().to(dev)
+    out = torch.empty((M, N), dtype=torch.float16, device=dev)
+    n_launch = 64
+    Wts = [(torch.rand((N, K), generator=g) * 0.04 - 0.02).half().to(dev) for _ in range(n_launch)]
+
+    def launches():
+        s = _lib.stream_ptr()
+        for i in range(n_launch):
+            _lib.call("kr_det_matmul", A.data_ptr(), M, K, Wts[i].data_ptr(), K, N, out.data_ptr(),
+                      N, 5, res.data_ptr(), gate.data_ptr(), s)
+
+    launches()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    stream = torch.cuda.Stream()
+    with torch.cuda.stream(stream):
+        with torch.cuda.graph(graph, stream=stream):
+            launches()
+    ms = []
+    with torch.cuda.stream(stream):
+        for _ in range(4):
+            e0 = torch.cuda.Event(enable_timing=True)
+            e1 = torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            graph.replay()
+            e1.record(stream)
+            e1.synchronize()
+            ms.append(e0.elapsed_time(e1))
+    avg_s = min(ms[1:]) / 1000.0 / n_launch
+    alg_bytes = K * N * 2 + M * K * 2 + 3 * M * N * 2
+    achieved = alg_bytes / avg_s / 1e9
+    traffic = None
+    tfile = os.path.join(ROOT, "profiles", "gemm_skinny_ffn_value_B256_traffic.json")
+    if os.path.exists(tfile) and M == 256:
+        with open(tfile) as f:
+            traffic = json.load(f).get("hbm_bytes_per_launch")
+    return {"kernel": "gemm_skinny_kernel<2,2> (stepped ffn value GEMM, M=%d K=%d N=%d, gated epilogue)"
+                      % (M, K, N),
+            "bound": "hbm", "achieved": round(achieved, 2), "peak": MI355X_HBM_PEAK / 1e9,
+            "unit": "GB/s", "frac": round(achieved / (MI355X_HBM_PEAK / 1e9), 4), "traffic": traffic,
+            "alg_bytes_per_launch": alg_bytes, "avg_launch_us": round(avg_s * 1e6, 3)}
+
+
+def cpu_baseline(weights16, args):
+    """The oracle (fp32 torch forward, numpy CDF, C range coder) on the host."""
+    import numpy as np
+    import torch
+    from krunch_amd import synthetic
+    from oracle import crc, rwkv4
+    from oracle import softmax as osm
+
+    torch.set_num_threads(os.cpu_count() or 1)
+    w = {k: v.float() for k, v in weights16.items()}
+    T = args.window
+    toks = synthetic.zipf_tokens(1, T, repeat_rate=0.05)
+    inp = synthetic.model_inputs(toks)
+    t0 = time.perf_counter()
+    st = rwkv4.new_state(12, 1, 768)
+    lg = rwkv4.forward(w, torch.as_tensor(inp), st)[0].numpy()
+    cdf = osm.logits_to_cdf(lg)
+    lo, hi = osm.sym_intervals(cdf, toks[0])
+    bits = crc.encode_intervals(lo, hi)
+    t_c = time.perf_counter() - t0
+    n_dec = min(args.cpu_decode_steps, T)
+    t0 = time.perf_counter()
+    st = rwkv4.new_state(12, 1, 768)
+    dec = crc.Decoder(bits)
+    last, got = 0, []
+    for _ in range(n_dec):
+        row = rwkv4.forward(w, torch.tensor([[last]]), st)[0]
+        c = osm.logits_to_cdf(row.numpy())[0]
+        t = dec.target()
+        sym = int(np.searchsorted(c, t, side="right") - 1)
+        dec.consume(int(c[sym]), int(c[sym + 1]))
+        got.append(sym)
+        last = sym
+    t_d = time.perf_counter() - t0
+    c_tok_s, d_tok_s = T / t_c, n_dec / t_d
+    rt = 1.0 / (1.0 / c_tok_s + 1.0 / d_tok_s)
+    cpu_model = platform.processor() or ""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                cpu_model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"value": round(rt * BYTES_PER_TOKEN / 1024, 3), "unit": "KB/s",
+            "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"1 chunk: packed compress of {T} tokens + {n_dec} stepped decode steps "
+                      f"(fp32 torch forward, numpy CDF, C range coder)",
+            "compress_tok_s": round(c_tok_s, 1), "decompress_tok_s": round(d_tok_s, 2),
+            "cpu_packed_stepped_bit_identical": bool(np.array_equal(np.array(got), toks[0, :n_dec])),
+            "cpu_model": cpu_model}
+
+
+def main():
+    args = parse()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py measures one MI355X only: every chunk is independent and this build "
+              "has no multi-GPU path (see DESIGN.md, 'How it would shard'). Run with --gpus 1.",
+              file=sys.stderr)
+        sys.exit(2)
+    import torch
+    from krunch_amd import synthetic
+    weights16 = synthetic.make_weights()
+    if args.kernel_probe:
+        kernel_probe(weights16, args.batch)
+        return
+    r = gpu_bench(args, weights16)
+    t = r["t_c"] + r["t_d"]
+    kb = r["ntok"] * BYTES_PER_TOKEN / 1024
+    res = {
+        "metric": "compress & decompress input KB/s per MI355X (169M shape, B=256); % of peak",
+        "value": round(kb / t, 2),
+        "unit": "KB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(1000 * t / args.steps, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp16",
+        "data": "synthetic (random-init RWKV-4-169M-shaped weights, Zipf(1.1) tokens, 5% repeats)",
+        "config": {"workload": "config5-window: B=256 chunks x 1024-token window, packed compress "
+                               "+ 1024-step stepped decompress, state carried across windows",
+                   "batch_chunks": args.batch, "window_tokens": args.window},
+        "compress_kbps": round(kb / r["t_c"], 2),
+        "decompress_kbps": round(kb / r["t_d"], 2),
+        "compress_tok_s": round(r["ntok"] / r["t_c"], 1),
+        "decompress_tok_s": round(r["ntok"] / r["t_d"], 1),
+        "compress_pflops": round(r["ntok"] * FLOP_PER_TOKEN / r["t_c"] / 1e15, 4),
+        "bits_per_token": round(8 * r["comp_bytes"] / r["total_tok"], 4),
+        "roundtrip_exact": r["exact"],
+    }
+    res["roofline"] = dominant_kernel_roofline(weights16, args.batch)
+    if not args.no_cpu_baseline:
+        res["cpu_baseline"] = cpu_baseline(weights16, args)
+    print(json.dumps(res))
+
+
+if __name__ == "__main__":
+    main()

@@ -35,7 +35,7 @@ class Workspace:
     def get(self, nbytes: int) -> torch.Tensor:
         if self.buf is None or self.buf.numel() < nbytes:
             self.buf = None
-            self.buf = torch.empty(nbytes, dtype=torch.uint8, device=self.device)
+            self.buf = torch.zeros(nbytes, dtype=torch.uint8, device=self.device)
         return self.buf
 
 

@@ -24,8 +24,27 @@ struct kr_gemm_args {
     int M, N, K;
 };
 
-// Launch C = A @ W (W given transposed) with the tile shape chosen from M.
-// Every output element is one chain of v_mfma_f32_16x16x32_f16 over
-// k = 0, 32, ..., K-32 starting from zero, whatever the tile shape, so a row
-// gets identical bits for any M.
+// The canonical reduction is split-K over 256-wide slices of K (K % 256 == 0).
+#define KR_GEMM_KSPLIT 256
+#define KR_GEMM_MAX_JOBS 3
+
+// Up to three products with the same M and K in one launch.
+struct kr_gemm_multi {
+    kr_gemm_args job[KR_GEMM_MAX_JOBS];
+    int ep[KR_GEMM_MAX_JOBS];
+    int tiles[KR_GEMM_MAX_JOBS];
+    int njobs;
+};
+
+// Launch C = A @ W (W given transposed), kernel and tile shape chosen from M.
+// Reduction contract, whatever the kernel: for every output element,
+//   P_s = chain of v_mfma_f32_16x16x32_f16 over k = 256s, 256s+32, ..., 256s+224
+//         starting from zero (s = 0 .. K/256 - 1),
+//   acc = P_0; acc = acc + P_1; ...; acc = acc + P_{S-1}   (fp32 adds, in order),
+// then the epilogue. A row therefore gets identical bits for any M.
 int kr_gemm_launch(const kr_gemm_args& g, int epilogue, hipStream_t stream);
+// Several products; on the small-M path those sharing M and K run in one
+// launch (independent outputs), otherwise they are launched in order.
+int kr_gemm_launch_multi(const kr_gemm_args* jobs, const int* epilogues, int njobs,
+                         hipStream_t stream);
+

@@ -12,6 +12,7 @@
 //   x = x + fp16(rf * fp16(kf@fVw))                         [GEMM, GATED]
 // Packed (T tokens per stream) and stepped (T = 1) calls run the same
 // kernels, so every row is computed by the same instruction sequence.
+#include <algorithm>
 #include <vector>
 
 #include "kr_gemm.h"
@@ -282,14 +283,16 @@ struct Work {
     float *k, *v;
 };
 
+inline size_t up256(size_t b) { return (b + 255) / 256 * 256; }
+
 size_t work_bytes(long long M, int C, int F) {
     const size_t h = (size_t)M * C * 2, f = (size_t)M * C * 4, kf = (size_t)M * F * 2;
-    return 8 * ((h + 255) / 256 * 256) + 2 * ((f + 255) / 256 * 256) + (kf + 255) / 256 * 256;
+    return 8 * up256(h) + 2 * up256(f) + up256(kf);
 }
 
 Work carve(void* ws, long long M, int C, int F) {
     char* p = static_cast<char*>(ws);
-    auto take = [&](size_t bytes) { char* q = p; p += (bytes + 255) / 256 * 256; return q; };
+    auto take = [&](size_t bytes) { char* q = p; p += up256(bytes); return q; };
     const size_t h = (size_t)M * C * 2, f = (size_t)M * C * 4;
     Work w;
     w.kx = reinterpret_cast<kr_half*>(take(h));
@@ -308,9 +311,9 @@ Work carve(void* ws, long long M, int C, int F) {
 
 int rows_per_run(int T) { return T >= 64 ? 16 : (T >= 8 ? 4 : 1); }
 
-int gemm(const kr_half* A, int M, int K, const void* Wt, int N, void* out, int ep, hipStream_t s,
-         const kr_half* res = nullptr, const kr_half* gate = nullptr) {
-    kr_gemm_args g;
+kr_gemm_args gemm_args(const kr_half* A, int M, int K, const void* Wt, int N, void* out,
+                       const kr_half* res = nullptr, const kr_half* gate = nullptr) {
+    kr_gemm_args g{};
     g.A = A;
     g.lda = K;
     g.Wt = H(Wt);
@@ -322,7 +325,7 @@ int gemm(const kr_half* A, int M, int K, const void* Wt, int N, void* out, int e
     g.M = M;
     g.N = N;
     g.K = K;
-    return kr_gemm_launch(g, ep, s);
+    return g;
 }
 
 #define KR_TRY(expr)              \
@@ -345,25 +348,33 @@ int layer_forward(const kr_layer_weights& L, int C, int F, kr_half* x, int B, in
     a.T = T;
     a.run = rows_per_run(T);
     KR_TRY(launch_ln_mix<3>(G, a, s));
-    KR_TRY(gemm(w.kx, M, C, L.Kt, C, w.k, KR_EP_F32, s));
-    KR_TRY(gemm(w.vx, M, C, L.Vt, C, w.v, KR_EP_F32, s));
-    KR_TRY(gemm(w.rx, M, C, L.Rt, C, w.r, KR_EP_SIGMOID, s));
+    {
+        const kr_gemm_args jobs[3] = {gemm_args(w.kx, M, C, L.Kt, C, w.k),
+                                      gemm_args(w.vx, M, C, L.Vt, C, w.v),
+                                      gemm_args(w.rx, M, C, L.Rt, C, w.r)};
+        const int eps[3] = {KR_EP_F32, KR_EP_F32, KR_EP_SIGMOID};
+        KR_TRY(kr_gemm_launch_multi(jobs, eps, 3, s));
+    }
     {
         dim3 grid((C + 255) / 256, B);
         wkv_kernel<<<grid, 256, 0, s>>>(w.k, w.v, w.r, L.decay, L.first, st.aa, st.bb, st.pp,
                                         w.ry, B, T, C);
         KR_LAUNCHED();
     }
-    KR_TRY(gemm(w.ry, M, C, L.Ot, C, x, KR_EP_RESID, s, x));
+    KR_TRY(kr_gemm_launch(gemm_args(w.ry, M, C, L.Ot, C, x, x), KR_EP_RESID, s));
     a.ln_w = H(L.ln2_w);
     a.ln_b = H(L.ln2_b);
     a.tm[0] = H(L.ftm_k); a.tm[1] = H(L.ftm_r);
     a.out[0] = w.fkx; a.out[1] = w.frx;
     a.state = Hm(st.ffn_xx);
     KR_TRY(launch_ln_mix<2>(G, a, s));
-    KR_TRY(gemm(w.frx, M, C, L.fRt, C, w.rf, KR_EP_SIGMOID, s));
-    KR_TRY(gemm(w.fkx, M, C, L.fKt, F, w.kf, KR_EP_RELUSQ, s));
-    KR_TRY(gemm(w.kf, M, F, L.fVt, C, x, KR_EP_GATED, s, x, w.rf));
+    {
+        const kr_gemm_args jobs[2] = {gemm_args(w.frx, M, C, L.fRt, C, w.rf),
+                                      gemm_args(w.fkx, M, C, L.fKt, F, w.kf)};
+        const int eps[2] = {KR_EP_SIGMOID, KR_EP_RELUSQ};
+        KR_TRY(kr_gemm_launch_multi(jobs, eps, 2, s));
+    }
+    KR_TRY(kr_gemm_launch(gemm_args(w.kf, M, F, L.fVt, C, x, x, w.rf), KR_EP_GATED, s));
     return KR_OK;
 }
 
@@ -434,7 +445,7 @@ int kr_impl_head(const kr_model_weights* m, const void* x, int M, void* xn, void
     a.T = 1;
     a.run = 1;
     KR_TRY(launch_ln_mix<0>(m->C / 256, a, s));
-    kr_gemm_args g;
+    kr_gemm_args g{};
     g.A = H(xn);
     g.lda = m->C;
     g.Wt = H(m->headT);

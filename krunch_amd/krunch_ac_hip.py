@@ -231,7 +231,7 @@ def rwkv4_layer_step_cpp(x, att_xx, aa, bb, pp, ffn_xx, ln1_w, ln1_b, tm_k, tm_v
         _cuda(t, dt, n)
     out = x.contiguous().clone()
     ws_bytes = _lib.lib().kr_forward_workspace_bytes(B * T, C, F)
-    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+    ws = torch.zeros(ws_bytes, dtype=torch.uint8, device=dev)
     _lib.call("kr_layer_step", L, C, F, out.data_ptr(), B, T, att_xx.data_ptr(), aa.data_ptr(),
               bb.data_ptr(), pp.data_ptr(), ffn_xx.data_ptr(), ws.data_ptr(), ws_bytes,
               _lib.stream_ptr())

@@ -34,9 +34,11 @@ def test_logits_match_fp32_oracle(model):
         np.testing.assert_allclose(st[3][i].cpu().numpy(), ost[i]["pp"].numpy(), atol=2e-2, rtol=1e-3)
 
 
-def test_packed_equals_stepped_and_windowed(model):
+@pytest.mark.parametrize("B,T", [(3, 40), (2, 600)])
+def test_packed_equals_stepped_and_windowed(model, B, T):
+    """(3, 40): both sides on the small-M kernel; (2, 600): packed on the
+    LDS-tiled kernel, stepped on the split-K small-M kernel."""
     _, W = model
-    B, T = 3, 40
     inp = synthetic.model_inputs(synthetic.zipf_tokens(B, T))
     st = cpp_path.fresh_state_batched(W, B)
     packed = cpp_path.forward_packed_batched(W, inp, st).view(B, T, -1)
