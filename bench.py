@@ -41,6 +41,8 @@ def parse():
     ap.add_argument("--window", type=int, default=1024)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-decode-steps", type=int, default=48)
+    ap.add_argument("--groups", type=int, default=1,
+                    help="decode the B streams as this many concurrent groups (graph branches)")
     ap.add_argument("--kernel-probe", action="store_true",
                     help="only run a 256 MiB device copy (counter calibration) and 8 launches of "
                          "the dominant kernel, for rocprofv3 --pmc runs")
@@ -133,7 +135,9 @@ def gpu_bench(args, weights16):
 
     # ----------------------------------------------------------- decompress
     del ws, x, logits, pairs
-    dws, dws_bytes = cpp_path.workspace(W, B)
+    G = max(1, min(args.groups, B))
+    dws_bytes = _lib.lib().kr_decode_workspace_bytes(B, G, P.C, P.F)
+    dws = torch.empty(dws_bytes, dtype=torch.uint8, device=dev)
     dx = torch.empty((B, P.C), dtype=torch.float16, device=dev)
     dlogits = torch.empty((B, P.V), dtype=torch.float16, device=dev)
     dac = torch.empty((B, 4), dtype=torch.uint32, device=dev)
@@ -148,7 +152,7 @@ def gpu_bench(args, weights16):
         _lib.call("kr_decode_run", P.ptr, B, dstate.ptr, syms.data_ptr(), dx.data_ptr(),
                   dws.data_ptr(), dws_bytes, dlogits.data_ptr(), P.V, out.data_ptr(), out.numel(),
                   base.data_ptr(), nbytes.data_ptr(), dac.data_ptr(), dtoks.data_ptr(), L,
-                  cnt.data_ptr(), None, PREC, n_steps, 1, s)
+                  cnt.data_ptr(), None, PREC, n_steps, G, 1, s)
 
     if args.warmup:
         decode(args.warmup * Tw)
@@ -318,7 +322,8 @@ def main():
         "data": "synthetic (random-init RWKV-4-169M-shaped weights, Zipf(1.1) tokens, 5% repeats)",
         "config": {"workload": "config5-window: B=256 chunks x 1024-token window, packed compress "
                                "+ 1024-step stepped decompress, state carried across windows",
-                   "batch_chunks": args.batch, "window_tokens": args.window},
+                   "batch_chunks": args.batch, "window_tokens": args.window,
+                   "decode_groups": args.groups},
         "compress_kbps": round(kb / r["t_c"], 2),
         "decompress_kbps": round(kb / r["t_d"], 2),
         "compress_tok_s": round(r["ntok"] / r["t_c"], 1),

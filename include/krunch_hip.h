@@ -133,8 +133,10 @@ int kr_softmax_cdf_decode(const uint16_t* logits, int B, int V, long long ld,
 
 /* ------------------------------------------------------------ GEMM / model
  * Matrices of the model are stored transposed, [out, in] (K contiguous).
- * Every output element is one chain of v_mfma_f32_16x16x32_f16 over K in
- * increasing order starting from 0, so results do not depend on M.
+ * Every output element is reduced the same way whatever M or the kernel:
+ * P_s = chain of v_mfma_f32_16x16x32_f16 over the 256-wide K slice s (from
+ * zero), acc = P_0 + P_1 + ... added left to right in fp32; so a row's
+ * result does not depend on how many rows share the call (K % 256 == 0).
  */
 
 /* W [K, N] (row stride ldw) -> Wt [N, K] (row stride ldt), fp16. */
@@ -229,15 +231,19 @@ int kr_decode_step(const kr_model_weights* m, int B, void* state, int32_t* syms,
                    long long tok_stride, int32_t* tok_count, const int32_t* n_tokens,
                    int cdf_precision, void* stream);
 
-/* n_steps decode steps; with use_graph the step is captured once into a HIP
- * graph and replayed (the reference's graph path, cpp_path.py:229-276).
- * Synchronous with respect to the work it enqueues. */
+/* n_steps decode steps. The B streams are split into n_groups groups of
+ * ceil(B/n_groups) streams with independent workspaces (ws_bytes >=
+ * kr_decode_workspace_bytes); with use_graph one step is captured into a HIP
+ * graph whose groups are parallel branches, so their latency-bound kernels
+ * overlap, and the graph is replayed n_steps times (the reference's graph
+ * path, cpp_path.py:229-276). Synchronous with respect to the work it enqueues. */
+size_t kr_decode_workspace_bytes(int B, int n_groups, int C, int F);
 int kr_decode_run(const kr_model_weights* m, int B, void* state, int32_t* syms, void* x,
                   void* ws, size_t ws_bytes, void* logits, long long ld,
                   const uint8_t* input_buf, uint32_t in_len, const int32_t* base_byte_offsets,
                   const int32_t* byte_limits, uint32_t* ac_states, int32_t* tokens,
                   long long tok_stride, int32_t* tok_count, const int32_t* n_tokens,
-                  int cdf_precision, int n_steps, int use_graph, void* stream);
+                  int cdf_precision, int n_steps, int n_groups, int use_graph, void* stream);
 
 #ifdef __cplusplus
 }

@@ -64,8 +64,9 @@ _SIGS = {
                             P, I, P], I),
     "kr_decode_step": ([ctypes.POINTER(KrModelWeights), I, P, P, P, P, SZ, P, LL, P, U32, P, P,
                         P, P, LL, P, P, I, P], I),
+    "kr_decode_workspace_bytes": ([I, I, I, I], SZ),
     "kr_decode_run": ([ctypes.POINTER(KrModelWeights), I, P, P, P, P, SZ, P, LL, P, U32, P, P,
-                       P, P, LL, P, P, I, I, I, P], I),
+                       P, P, LL, P, P, I, I, I, I, P], I),
 }
 
 _lib = None

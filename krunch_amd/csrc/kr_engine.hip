@@ -17,6 +17,8 @@
 
 int kr_impl_forward_layers(const kr_model_weights* m, void* x, int B, int T, void* state,
                            void* ws, size_t ws_bytes, hipStream_t s);
+int kr_impl_forward_layers_view(const kr_model_weights* m, void* x, int B, int T, void* state,
+                                int state_B, int b0, void* ws, size_t ws_bytes, hipStream_t s);
 int kr_impl_embed(const kr_model_weights* m, const int32_t* ids, int M, void* x, hipStream_t s);
 int kr_impl_head(const kr_model_weights* m, const void* x, int M, void* xn, void* logits,
                  long long ld, hipStream_t s);
@@ -79,11 +81,14 @@ struct DecodeStepArgs {
     int32_t* tok_count;
     const int32_t* n_tokens;
     int prec;
+    int state_B;   // streams held by `state` (>= b0 + B)
+    int b0;        // first stream of this call within `state`
 };
 
 int decode_step(const DecodeStepArgs& a, hipStream_t s) {
     KR_TRY(kr_impl_embed(a.m, a.syms, a.B, a.x, s));
-    KR_TRY(kr_impl_forward_layers(a.m, a.x, a.B, 1, a.state, a.ws, a.ws_bytes, s));
+    KR_TRY(kr_impl_forward_layers_view(a.m, a.x, a.B, 1, a.state, a.state_B, a.b0, a.ws,
+                                       a.ws_bytes, s));
     void* xn = kr_impl_head_scratch(a.ws, a.B, a.m->C, a.m->F);
     KR_TRY(kr_impl_head(a.m, a.x, a.B, xn, a.logits, a.ld, s));
     return kr_softmax_cdf_decode(reinterpret_cast<const uint16_t*>(a.logits), a.B, a.m->V, a.ld,
@@ -160,43 +165,77 @@ int kr_decode_step(const kr_model_weights* m, int B, void* state, int32_t* syms,
                    const int32_t* n_tokens, int cdf_precision, void* stream) {
     DecodeStepArgs a{m, B, state, syms, x, ws, ws_bytes, logits, ld, input_buf, in_len,
                      base_byte_offsets, byte_limits, ac_states, tokens, tok_stride, tok_count,
-                     n_tokens, cdf_precision};
+                     n_tokens, cdf_precision, B, 0};
     KR_TRY(check_decode(a));
     return decode_step(a, kr_stream(stream));
+}
+
+size_t kr_decode_workspace_bytes(int B, int n_groups, int C, int F) {
+    if (B < 1 || n_groups < 1) return 0;
+    const int G = n_groups > B ? B : n_groups;
+    const int Bg = (B + G - 1) / G;
+    const size_t per = (kr_impl_work_bytes(Bg, C, F) + 255) / 256 * 256;
+    return per * (size_t)G;
 }
 
 int kr_decode_run(const kr_model_weights* m, int B, void* state, int32_t* syms, void* x,
                   void* ws, size_t ws_bytes, void* logits, long long ld, const uint8_t* input_buf,
                   uint32_t in_len, const int32_t* base_byte_offsets, const int32_t* byte_limits,
                   uint32_t* ac_states, int32_t* tokens, long long tok_stride, int32_t* tok_count,
-                  const int32_t* n_tokens, int cdf_precision, int n_steps, int use_graph,
-                  void* stream) {
-    DecodeStepArgs a{m, B, state, syms, x, ws, ws_bytes, logits, ld, input_buf, in_len,
-                     base_byte_offsets, byte_limits, ac_states, tokens, tok_stride, tok_count,
-                     n_tokens, cdf_precision};
-    KR_TRY(check_decode(a));
+                  const int32_t* n_tokens, int cdf_precision, int n_steps, int n_groups,
+                  int use_graph, void* stream) {
+    KR_REQUIRE(m && B >= 1 && n_groups >= 1 && n_groups <= 16, "kr_decode_run: bad B/n_groups");
     KR_REQUIRE(n_steps >= 0, "kr_decode_run: bad n_steps");
+    const int G = n_groups > B ? B : n_groups;
+    const int Bg = (B + G - 1) / G;
+    const size_t per_ws = (kr_impl_work_bytes(Bg, m->C, m->F) + 255) / 256 * 256;
+    KR_REQUIRE(ws_bytes >= per_ws * G, "kr_decode_run: workspace too small (need %zu)", per_ws * G);
+    // One argument set per group of streams [b0, b0 + Bg).
+    DecodeStepArgs grp[16];
+    int ng = 0;
+    for (int b0 = 0; b0 < B; b0 += Bg, ng++) {
+        const int n = B - b0 < Bg ? B - b0 : Bg;
+        DecodeStepArgs a{m, n, state, syms + b0,
+                         static_cast<char*>(x) + (size_t)b0 * m->C * 2,
+                         static_cast<char*>(ws) + per_ws * ng, per_ws,
+                         static_cast<char*>(logits) + (size_t)b0 * ld * 2, ld, input_buf, in_len,
+                         base_byte_offsets ? base_byte_offsets + b0 : nullptr,
+                         byte_limits ? byte_limits + b0 : nullptr, ac_states + 4 * (size_t)b0,
+                         tokens ? tokens + (size_t)b0 * tok_stride : nullptr, tok_stride,
+                         tok_count ? tok_count + b0 : nullptr, n_tokens ? n_tokens + b0 : nullptr,
+                         cdf_precision, B, b0};
+        KR_TRY(check_decode(a));
+        grp[ng] = a;
+    }
     hipStream_t s = kr_stream(stream);
     if (n_steps == 0) return KR_OK;
     if (!use_graph) {
-        for (int i = 0; i < n_steps; i++) KR_TRY(decode_step(a, s));
+        for (int i = 0; i < n_steps; i++)
+            for (int g = 0; g < ng; g++) KR_TRY(decode_step(grp[g], s));
         return KR_OK;
     }
     // Warm per-V caches (CDF summation plan) outside the capture: a
     // zero-row launch builds the plan without running a kernel.
     KR_TRY(kr_probs_to_cdf(reinterpret_cast<const float*>(logits), 0, m->V, m->V, ac_states,
                            cdf_precision, stream));
-    hipStream_t cap = nullptr;
-    hipEvent_t ev_in = nullptr, ev_out = nullptr;
+    // One graph per step: the groups are independent branches (fork/join
+    // through events), so their latency-bound kernels overlap on the GPU.
+    hipStream_t cap[16] = {};
+    hipEvent_t ev[18] = {};
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
     int rc = KR_OK;
+    bool capturing = false;
     auto cleanup = [&]() {
+        if (capturing) {
+            hipGraph_t g2 = nullptr;
+            (void)hipStreamEndCapture(cap[0], &g2);
+            if (g2) (void)hipGraphDestroy(g2);
+        }
         if (exec) (void)hipGraphExecDestroy(exec);
         if (graph) (void)hipGraphDestroy(graph);
-        if (ev_in) (void)hipEventDestroy(ev_in);
-        if (ev_out) (void)hipEventDestroy(ev_out);
-        if (cap) (void)hipStreamDestroy(cap);
+        for (auto& e : ev) if (e) (void)hipEventDestroy(e);
+        for (auto& c : cap) if (c) (void)hipStreamDestroy(c);
     };
     auto hip_fail = [&](hipError_t e, const char* what) {
         rc = kr_fail(KR_EHIP, "kr_decode_run: %s: %s", what, hipGetErrorString(e));
@@ -204,24 +243,37 @@ int kr_decode_run(const kr_model_weights* m, int B, void* state, int32_t* syms, 
         return rc;
     };
     hipError_t e;
-    if ((e = hipStreamCreateWithFlags(&cap, hipStreamNonBlocking)) != hipSuccess) return hip_fail(e, "stream");
-    if ((e = hipEventCreateWithFlags(&ev_in, hipEventDisableTiming)) != hipSuccess) return hip_fail(e, "event");
-    if ((e = hipEventCreateWithFlags(&ev_out, hipEventDisableTiming)) != hipSuccess) return hip_fail(e, "event");
-    if ((e = hipEventRecord(ev_in, s)) != hipSuccess) return hip_fail(e, "record");
-    if ((e = hipStreamWaitEvent(cap, ev_in, 0)) != hipSuccess) return hip_fail(e, "wait");
-    if ((e = hipStreamBeginCapture(cap, hipStreamCaptureModeThreadLocal)) != hipSuccess)
+    for (int g = 0; g < ng; g++)
+        if ((e = hipStreamCreateWithFlags(&cap[g], hipStreamNonBlocking)) != hipSuccess)
+            return hip_fail(e, "stream");
+    for (int i = 0; i < ng + 2; i++)
+        if ((e = hipEventCreateWithFlags(&ev[i], hipEventDisableTiming)) != hipSuccess)
+            return hip_fail(e, "event");
+    // ev[0]: caller -> capture stream; ev[1]: fork; ev[2+g]: join of group g; ev[ng+1] reused at the end
+    if ((e = hipEventRecord(ev[0], s)) != hipSuccess) return hip_fail(e, "record");
+    if ((e = hipStreamWaitEvent(cap[0], ev[0], 0)) != hipSuccess) return hip_fail(e, "wait");
+    if ((e = hipStreamBeginCapture(cap[0], hipStreamCaptureModeThreadLocal)) != hipSuccess)
         return hip_fail(e, "begin capture");
-    rc = decode_step(a, cap);
-    e = hipStreamEndCapture(cap, &graph);
+    capturing = true;
+    if ((e = hipEventRecord(ev[1], cap[0])) != hipSuccess) return hip_fail(e, "fork record");
+    for (int g = 1; g < ng; g++)
+        if ((e = hipStreamWaitEvent(cap[g], ev[1], 0)) != hipSuccess) return hip_fail(e, "fork wait");
+    for (int g = 0; g < ng && rc == KR_OK; g++) rc = decode_step(grp[g], cap[g]);
     if (rc) { cleanup(); return rc; }
+    for (int g = 1; g < ng; g++) {
+        if ((e = hipEventRecord(ev[1 + g], cap[g])) != hipSuccess) return hip_fail(e, "join record");
+        if ((e = hipStreamWaitEvent(cap[0], ev[1 + g], 0)) != hipSuccess) return hip_fail(e, "join wait");
+    }
+    e = hipStreamEndCapture(cap[0], &graph);
+    capturing = false;
     if (e != hipSuccess) return hip_fail(e, "end capture");
     if ((e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0)) != hipSuccess)
         return hip_fail(e, "instantiate");
     for (int i = 0; i < n_steps; i++)
-        if ((e = hipGraphLaunch(exec, cap)) != hipSuccess) return hip_fail(e, "graph launch");
-    if ((e = hipEventRecord(ev_out, cap)) != hipSuccess) return hip_fail(e, "record");
-    if ((e = hipStreamWaitEvent(s, ev_out, 0)) != hipSuccess) return hip_fail(e, "wait");
-    if ((e = hipStreamSynchronize(cap)) != hipSuccess) return hip_fail(e, "sync");
+        if ((e = hipGraphLaunch(exec, cap[0])) != hipSuccess) return hip_fail(e, "graph launch");
+    if ((e = hipEventRecord(ev[ng + 1], cap[0])) != hipSuccess) return hip_fail(e, "record");
+    if ((e = hipStreamWaitEvent(s, ev[ng + 1], 0)) != hipSuccess) return hip_fail(e, "wait");
+    if ((e = hipStreamSynchronize(cap[0])) != hipSuccess) return hip_fail(e, "sync");
     cleanup();
     return KR_OK;
 }

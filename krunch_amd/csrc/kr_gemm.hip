@@ -165,16 +165,6 @@ __global__ void __launch_bounds__(256, 2) gemm_tile_kernel(kr_gemm_args g) {
 // ---------------------------------------------------------------------------
 // Skinny kernel (small M)
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ void store_rt(const kr_gemm_args& g, int ep, int m, int n, float acc) {
-    switch (ep) {
-        case KR_EP_F32: store_one<KR_EP_F32>(g, m, n, acc); break;
-        case KR_EP_F16: store_one<KR_EP_F16>(g, m, n, acc); break;
-        case KR_EP_SIGMOID: store_one<KR_EP_SIGMOID>(g, m, n, acc); break;
-        case KR_EP_RELUSQ: store_one<KR_EP_RELUSQ>(g, m, n, acc); break;
-        case KR_EP_RESID: store_one<KR_EP_RESID>(g, m, n, acc); break;
-        default: store_one<KR_EP_GATED>(g, m, n, acc); break;
-    }
-}
 
 // One workgroup per (16*TM) x (16*TN) output tile of one job, one wave per
 // 256-wide K slice (S = K/256 waves). A wave first issues every operand load
@@ -186,13 +176,36 @@ template <int TM, int TN>
 __global__ void __launch_bounds__(768) gemm_skinny_kernel(kr_gemm_multi mj) {
     extern __shared__ __attribute__((aligned(16))) float part_lds[];   // [S][TM*TN][256]
     const int lane = threadIdx.x & 63, s = threadIdx.x >> 6;
-    int tile = blockIdx.x, j = 0;
-    while (j + 1 < mj.njobs && tile >= mj.tiles[j]) { tile -= mj.tiles[j]; j++; }
-    const kr_gemm_args& g = mj.job[j];
-    const int ep = mj.ep[j];
+    // Job of this workgroup; fields are copied with constant indices so every
+    // kernel-argument load is issued up front (no dependent scalar loads).
+    const int bid = blockIdx.x;
+    const int j = bid < mj.tiles[0] ? 0 : (bid < mj.tiles[0] + mj.tiles[1] ? 1 : 2);
+    const int tile = bid - (j > 0 ? mj.tiles[0] : 0) - (j > 1 ? mj.tiles[1] : 0);
+    kr_gemm_args g;
+    int ep;
+    if (j == 0) { g = mj.job[0]; ep = mj.ep[0]; }
+    else if (j == 1) { g = mj.job[1]; ep = mj.ep[1]; }
+    else { g = mj.job[2]; ep = mj.ep[2]; }
     const int S = g.K / kKS;
     const int ntn = (g.N + 16 * TN - 1) / (16 * TN);
     const int m0 = (tile / ntn) * 16 * TM, n0 = (tile % ntn) * 16 * TN;
+    // Wave 0 applies the epilogue; fetch its residual / gate operands now so
+    // their latency overlaps the operand loads.
+    kr_half4 res_v[TM][TN], gate_v[TM][TN];
+    if (s == 0 && (ep == KR_EP_RESID || ep == KR_EP_GATED)) {
+        #pragma unroll
+        for (int i = 0; i < TM; i++)
+            #pragma unroll
+            for (int t = 0; t < TN; t++)
+                #pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const int m = min(m0 + 16 * i + (lane >> 4) * 4 + r, g.M - 1);
+                    const int n = min(n0 + 16 * t + (lane & 15), g.N - 1);
+                    const size_t o = (size_t)m * (size_t)g.ldo + (size_t)n;
+                    res_v[i][t][r] = g.res[o];
+                    gate_v[i][t][r] = ep == KR_EP_GATED ? g.gate[o] : (kr_half)0.0f;
+                }
+    }
     const int k0 = s * kKS + (lane >> 4) * 8;
     kr_half8 a[TM][8], b[TN][8];
     #pragma unroll
@@ -248,7 +261,21 @@ __global__ void __launch_bounds__(768) gemm_skinny_kernel(kr_gemm_multi mj) {
             for (int r = 0; r < 4; r++) {
                 const int m = m0 + 16 * i + (lane >> 4) * 4 + r;
                 const int n = n0 + 16 * t + (lane & 15);
-                if (m < g.M && n < g.N) store_rt(g, ep, m, n, p[i][t][r]);
+                if (m >= g.M || n >= g.N) continue;
+                const size_t o = (size_t)m * (size_t)g.ldo + (size_t)n;
+                const float acc = p[i][t][r];
+                if (ep == KR_EP_F32) {
+                    reinterpret_cast<float*>(g.out)[o] = acc;
+                    continue;
+                }
+                const float h = (float)(kr_half)acc;
+                float y;
+                if (ep == KR_EP_F16) y = h;
+                else if (ep == KR_EP_SIGMOID) y = kr_sigmoid(h);
+                else if (ep == KR_EP_RELUSQ) { const float rr = h > 0.0f ? h : 0.0f; y = rr * rr; }
+                else if (ep == KR_EP_RESID) y = (float)res_v[i][t][r] + h;
+                else y = (float)res_v[i][t][r] + (float)(kr_half)((float)gate_v[i][t][r] * h);
+                reinterpret_cast<kr_half*>(g.out)[o] = (kr_half)y;
             }
 }
 

@@ -418,6 +418,30 @@ int kr_impl_forward_layers(const kr_model_weights* m, void* x, int B, int T, voi
     return KR_OK;
 }
 
+// The layer stack for streams [b0, b0 + B) of a state buffer holding state_B
+// streams (one group of a larger batch; rows of each [state_B, C] component).
+int kr_impl_forward_layers_view(const kr_model_weights* m, void* x, int B, int T, void* state,
+                                int state_B, int b0, void* ws, size_t ws_bytes, hipStream_t s) {
+    KR_TRY(check_model(m));
+    KR_REQUIRE(x && state && ws, "forward: null pointer");
+    KR_REQUIRE(b0 >= 0 && B >= 1 && b0 + B <= state_B, "forward: bad stream range");
+    const long long M = (long long)B * T;
+    KR_REQUIRE(T >= 1 && M <= (1ll << 31) / m->F, "forward: bad T=%d", T);
+    KR_REQUIRE(ws_bytes >= work_bytes(M, m->C, m->F), "forward: workspace too small");
+    const Work w = carve(ws, M, m->C, m->F);
+    const size_t off = (size_t)b0 * m->C;
+    for (int i = 0; i < m->n_layer; i++) {
+        kr_layer_state st = state_of(state, i, state_B, m->C);
+        st.att_xx = static_cast<kr_half*>(st.att_xx) + off;
+        st.ffn_xx = static_cast<kr_half*>(st.ffn_xx) + off;
+        st.aa += off;
+        st.bb += off;
+        st.pp += off;
+        KR_TRY(layer_forward(m->layers[i], m->C, m->F, Hm(x), B, T, st, w, s));
+    }
+    return KR_OK;
+}
+
 int kr_impl_embed(const kr_model_weights* m, const int32_t* ids, int M, void* x, hipStream_t s) {
     if (M == 0) return KR_OK;
     const int blocks = (M + 3) / 4, G = m->C / 256;

@@ -61,6 +61,9 @@ class InferenceEngine:
         self._ready = False
         self.window = int(os.environ.get("KRUNCH_FORWARD_BATCH", "1024"))
         self.use_graph = os.environ.get("KRUNCH_HIP_GRAPH", "1") == "1"
+        # lockstep streams may be split into concurrent groups (graph branches); one
+        # group measured fastest on MI355X (branches of one graph do not overlap)
+        self.decode_groups = int(os.environ.get("KRUNCH_DECODE_GROUPS", "1"))
 
     # ------------------------------------------------------------------ setup
     def load(self, weights: Optional[dict] = None, tokenizer_path: Optional[str] = None,
@@ -184,12 +187,14 @@ class InferenceEngine:
         count = torch.zeros(B, dtype=torch.int32, device=dev)
         ntd = torch.tensor(n_tok, dtype=torch.int32, device=dev)
         x = torch.empty((B, P.C), dtype=torch.float16, device=dev)
-        ws, nbytes = cpp_path.workspace(W, B)
+        G = max(1, min(self.decode_groups, B))
+        nbytes = _lib.lib().kr_decode_workspace_bytes(B, G, P.C, P.F)
+        ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
         logits = torch.empty((B, P.V), dtype=torch.float16, device=dev)
         _lib.call("kr_decode_run", P.ptr, B, state.ptr, syms.data_ptr(), x.data_ptr(),
                   ws.data_ptr(), nbytes, logits.data_ptr(), P.V, inbuf.data_ptr(), inbuf.numel(),
                   base.data_ptr(), limits.data_ptr(), ac.data_ptr(), tokens.data_ptr(), Tmax,
-                  count.data_ptr(), ntd.data_ptr(), CDF_PRECISION, Tmax,
+                  count.data_ptr(), ntd.data_ptr(), CDF_PRECISION, Tmax, G,
                   1 if self.use_graph else 0, s)
         host = tokens.cpu().numpy()
         return [host[b, :n_tok[b]].copy() for b in range(B)]

@@ -36,6 +36,21 @@ def test_roundtrip_ragged_streams(eng):
         np.testing.assert_array_equal(d, t)
 
 
+def test_decode_groups_and_graph_agree(eng):
+    """Concurrent decode groups (graph branches) and the eager path decode the
+    same tokens as one group."""
+    toks = [synthetic.zipf_tokens(1, n, seed_base=900 + i)[0] for i, n in enumerate([90, 33, 70, 12, 64, 5, 41])]
+    enc = eng.compress_tokens_batched(toks)
+    outs = []
+    for groups, graph in ((1, True), (3, True), (7, True), (4, False)):
+        eng.decode_groups, eng.use_graph = groups, graph
+        outs.append(eng.decompress_tokens_batched(enc))
+    eng.decode_groups, eng.use_graph = 4, True
+    for dec in outs:
+        for t, d in zip(toks, dec):
+            np.testing.assert_array_equal(d, t)
+
+
 def test_repeated_spans_roundtrip(eng):
     toks = synthetic.zipf_tokens(3, 640, repeat_rate=0.3)
     enc = eng.compress_tokens_batched(list(toks))
