@@ -66,10 +66,12 @@ def kernel_probe(weights16, B):
     res = torch.randn((M, N), device=dev).half()
     gate = torch.rand((M, N), device=dev).half()
     out = torch.empty((M, N), dtype=torch.float16, device=dev)
-    Wt = P.tensors["0.fVt"]
+    Wf = P.tensors["0.fVf"]
+    Af = torch.empty(_lib.lib().kr_fragment_bytes(M, K) // 2, dtype=torch.float16, device=dev)
+    _lib.call("kr_pack_fragments", A.data_ptr(), K, M, K, Af.data_ptr(), _lib.stream_ptr())
     for _ in range(8):
-        _lib.call("kr_det_matmul", A.data_ptr(), M, K, Wt.data_ptr(), K, N, out.data_ptr(), N, 5,
-                  res.data_ptr(), gate.data_ptr(), _lib.stream_ptr())
+        _lib.call("kr_det_matmul_packed", Af.data_ptr(), M, K, Wf.data_ptr(), N, out.data_ptr(), N,
+                  5, res.data_ptr(), gate.data_ptr(), 0, _lib.stream_ptr())
     torch.cuda.synchronize()
     print(json.dumps({"probe": "ok", "copy_bytes": 2 * src.numel() * 4}))
 
@@ -172,7 +174,8 @@ def gpu_bench(args, weights16):
 def dominant_kernel_roofline(weights16, B):
     """Live roofline of the dominant kernel of the timed region: the stepped
     channel-mix value GEMM (M = B rows, K = 3072, N = 768, gated-residual
-    epilogue; the small-M MFMA kernel), 12 launches per decode step.
+    epilogue; the small-M MFMA kernel on fragment-packed operands, exactly as
+    the decode step launches it), 12 launches per decode step.
 
     It is HBM-bound: algorithmic bytes per launch = W (K*N*2) + A (M*K*2) +
     residual, gate and output (3*M*N*2). The average launch duration is
@@ -197,13 +200,22 @@ def dominant_kernel_roofline(weights16, B):
     gate = torch.rand((M, N), generator=g).half().to(dev)
     out = torch.empty((M, N), dtype=torch.float16, device=dev)
     n_launch = 64
-    Wts = [(torch.rand((N, K), generator=g) * 0.04 - 0.02).half().to(dev) for _ in range(n_launch)]
+
+    def packed(X):
+        R = X.shape[0]
+        buf = torch.empty(_lib.lib().kr_fragment_bytes(R, K) // 2, dtype=torch.float16, device=dev)
+        _lib.call("kr_pack_fragments", X.data_ptr(), K, R, K, buf.data_ptr(), _lib.stream_ptr())
+        return buf
+
+    Af = packed(A)
+    Wfs = [packed((torch.rand((N, K), generator=g) * 0.04 - 0.02).half().to(dev))
+           for _ in range(n_launch)]
 
     def launches():
         s = _lib.stream_ptr()
         for i in range(n_launch):
-            _lib.call("kr_det_matmul", A.data_ptr(), M, K, Wts[i].data_ptr(), K, N, out.data_ptr(),
-                      N, 5, res.data_ptr(), gate.data_ptr(), s)
+            _lib.call("kr_det_matmul_packed", Af.data_ptr(), M, K, Wfs[i].data_ptr(), N,
+                      out.data_ptr(), N, 5, res.data_ptr(), gate.data_ptr(), 0, s)
 
     launches()
     torch.cuda.synchronize()

@@ -151,6 +151,24 @@ int kr_det_matmul(const uint16_t* x, int M, int K, const uint16_t* Wt, long long
                   void* out, long long ldo, int epilogue, const uint16_t* res,
                   const uint16_t* gate, void* stream);
 
+/* Fragment-packed copy of Wt [N, K] (row stride ld) for the small-M GEMM: each
+ * 16-row x 32-column block is one contiguous 1 KB run in MFMA operand order
+ * (no reference counterpart: the reference's WMMA kernels read row-major
+ * weights, layer_cpp.cpp:206-290). Output holds kr_fragment_bytes(N, K) bytes,
+ * rows padded to a multiple of 16 with zeros; K % 32 == 0. */
+size_t kr_fragment_bytes(int N, int K);
+int kr_pack_fragments(const uint16_t* Wt, long long ld, int N, int K, uint16_t* out,
+                      void* stream);
+
+/* kr_det_matmul on fragment-packed operands (the stepped decode's GEMM): xf is
+ * x [M, K] packed by kr_pack_fragments (rows padded to 16), Wf is Wt [N, K]
+ * packed; M <= 512, N < 16384. out_packed = 1 writes an fp16 result packed as
+ * an [M, N] operand of the next product (elementwise fp16 epilogues only,
+ * N % 32 == 0). Same bits as kr_det_matmul on the unpacked operands. */
+int kr_det_matmul_packed(const uint16_t* xf, int M, int K, const uint16_t* Wf, int N, void* out,
+                         long long ldo, int epilogue, const uint16_t* res, const uint16_t* gate,
+                         int out_packed, void* stream);
+
 typedef struct kr_layer_weights {
     const void *ln1_w, *ln1_b;            /* fp16 [C] */
     const void *tm_k, *tm_v, *tm_r;       /* fp16 [C] */
@@ -162,6 +180,9 @@ typedef struct kr_layer_weights {
     const void *fKt;                      /* fp16 [F, C] */
     const void *fVt;                      /* fp16 [C, F] */
     const void *fRt;                      /* fp16 [C, C] */
+    /* Fragment-packed copies of the seven matrices above (kr_pack_fragments),
+     * read by the small-M (B*T <= 512) path; all NULL = use the row-major ones. */
+    const void *Kf, *Vf, *Rf, *Of, *fKf, *fVf, *fRf;
 } kr_layer_weights;
 
 typedef struct kr_model_weights {

@@ -21,7 +21,8 @@ SZ = ctypes.c_size_t
 class KrLayerWeights(ctypes.Structure):
     _fields_ = [(n, P) for n in (
         "ln1_w", "ln1_b", "tm_k", "tm_v", "tm_r", "decay", "first",
-        "Kt", "Vt", "Rt", "Ot", "ln2_w", "ln2_b", "ftm_k", "ftm_r", "fKt", "fVt", "fRt")]
+        "Kt", "Vt", "Rt", "Ot", "ln2_w", "ln2_b", "ftm_k", "ftm_r", "fKt", "fVt", "fRt",
+        "Kf", "Vf", "Rf", "Of", "fKf", "fVf", "fRf")]
 
 
 class KrModelWeights(ctypes.Structure):
@@ -51,6 +52,9 @@ _SIGS = {
     # GEMM / layers / model
     "kr_transpose_f16": ([P, LL, I, I, P, LL, P], I),
     "kr_det_matmul": ([P, I, I, P, LL, I, P, LL, I, P, P, P], I),
+    "kr_fragment_bytes": ([I, I], ctypes.c_size_t),
+    "kr_pack_fragments": ([P, LL, I, I, P, P], I),
+    "kr_det_matmul_packed": ([P, I, I, P, I, P, LL, I, P, P, I, P], I),
     "kr_prepare_decay": ([P, P, I, P], I),
     "kr_state_bytes": ([I, I, I], SZ),
     "kr_state_init": ([P, I, I, I, P], I),

@@ -112,7 +112,7 @@ extern "C" {
 
 const char* kr_last_error(void) { return g_err.c_str(); }
 
-int kr_abi_version(void) { return 1; }
+int kr_abi_version(void) { return 2; }
 
 size_t kr_forward_workspace_bytes(long long M, int C, int F) {
     return kr_impl_work_bytes(M, C, F);

@@ -13,20 +13,40 @@ enum kr_epilogue : int {
 };
 
 struct kr_gemm_args {
-    const kr_half* A;   // [M, K] row-major, row stride lda
+    const kr_half* A;   // [M, K] row-major, row stride lda (or fragment-packed, a_frag)
     long long lda;
     const kr_half* Wt;  // [N, K] row-major (W transposed), row stride ldw
     long long ldw;
-    void* out;          // [M, N], row stride ldo (f32 or f16 per epilogue)
+    void* out;          // [M, N], row stride ldo (f32 or f16 per epilogue; or fragment-packed)
     long long ldo;
     const kr_half* res;   // [M, N] stride ldo (RESID, GATED); may alias out
     const kr_half* gate;  // [M, N] stride ldo (GATED)
     int M, N, K;
+    const kr_half* Wf;  // W^T fragment-packed (kr_frag_index), or null; small-M path only
+    int a_frag;         // A is fragment-packed (small-M path only; needs Wf)
+    int out_frag;       // fp16 output written fragment-packed as a K = N operand
 };
+
+// Fragment-packed layout of an [R, K] fp16 operand (K % 32 == 0, R padded to
+// a multiple of 16): the 16 x 32 block (R/16 = rb, K/32 = kb) is one
+// contiguous 1 KB run at block index rb * (K/32) + kb, stored in the order
+// the v_mfma_f32_16x16x32_f16 operand registers want it: lane
+// l = (r % 16) + 16 * ((k % 32) / 8) holds the 8 halves k % 8 = 0..7. One
+// wave's operand load is then a single fully coalesced 1 KB read.
+__host__ __device__ inline size_t kr_frag_index(long long r, long long k, long long K) {
+    return ((size_t)((r >> 4) * (K >> 5) + (k >> 5)) * 64 +
+            (size_t)((r & 15) + 16 * ((k & 31) >> 3))) * 8 + (size_t)(k & 7);
+}
+// Rows of a fragment-packed operand with R logical rows (multiple of 16).
+__host__ __device__ inline long long kr_frag_rows(long long R) { return (R + 15) / 16 * 16; }
 
 // The canonical reduction is split-K over 256-wide slices of K (K % 256 == 0).
 #define KR_GEMM_KSPLIT 256
 #define KR_GEMM_MAX_JOBS 3
+// Products with M <= KR_GEMM_SMALL_M (and N < 16384) take the small-M kernel,
+// which also reads and writes fragment-packed operands.
+#define KR_GEMM_SMALL_M 512
+#define KR_GEMM_SMALL_MAX_N 16384
 
 // Up to three products with the same M and K in one launch.
 struct kr_gemm_multi {

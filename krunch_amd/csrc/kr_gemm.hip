@@ -12,11 +12,14 @@
 //    (row pitch 72 halves: the 16 rows read by one ds_read_b128 land on
 //    distinct banks) with the next slice's global loads in flight; the
 //    running slice accumulator is folded into the total every 256 K.
-//  * skinny kernel (small M): one workgroup per 16 x (16*TN) output tile,
-//    one wave per K slice; operands are loaded straight from global memory
-//    (A is small and L2-resident, W streams once), 8 MFMAs per slice; the
-//    slice partials are added in slice order through LDS by wave 0, which
-//    applies the epilogue. Parallelism comes from the K slices, not from M.
+//  * panel kernel (small M): one workgroup per (16*TM) x (16*NS) output
+//    tile, one wave per K slice; operands are loaded straight from global
+//    memory (fragment-packed on the decode path), A once and the NS weight
+//    panels streamed, 8 MFMAs per (row block, panel); the slice partials are
+//    added in slice order through LDS and the epilogue is shared out over the
+//    waves. Parallelism comes from the K slices, not from M.
+#include <algorithm>
+
 #include "kr_gemm.h"
 
 namespace {
@@ -163,120 +166,217 @@ __global__ void __launch_bounds__(256, 2) gemm_tile_kernel(kr_gemm_args g) {
 }
 
 // ---------------------------------------------------------------------------
-// Skinny kernel (small M)
+// Panel kernel (small M)
 // ---------------------------------------------------------------------------
 
-// One workgroup per (16*TM) x (16*TN) output tile of one job, one wave per
-// 256-wide K slice (S = K/256 waves). A wave first issues every operand load
-// of its slice (A rows are small and L2-resident; W streams once), then runs
-// the 8-deep MFMA chains; the slice partials meet in LDS and wave 0 adds them
-// in slice order and applies the job's epilogue. Several jobs with the same
-// M and K (e.g. the K, V, R projections) share one launch.
-template <int TM, int TN>
-__global__ void __launch_bounds__(768) gemm_skinny_kernel(kr_gemm_multi mj) {
-    extern __shared__ __attribute__((aligned(16))) float part_lds[];   // [S][TM*TN][256]
+// One workgroup per (16*TM) x (16*NS) output tile of one job, one wave per
+// 256-wide K slice (S = K/256 waves). A wave loads its slice of the TM A
+// fragments once, then streams NS weight panels of 16 columns (double
+// buffered), running one 8-deep MFMA chain per (row block, panel). The slice
+// partials meet in LDS; the TM*NS result tiles are then shared out over the
+// waves, each adding the S partials of a tile in slice order and applying the
+// job's epilogue. Several jobs with the same M and K (e.g. the K, V, R
+// projections) share one launch.
+//
+// Time on MI355X is set by the L2 requests a CU has in flight (about 64 lines
+// at ~470 cycles each), so the tile shape is chosen on the host to minimise
+// the operand bytes the busiest CU reads: a larger NS re-reads A less often.
+//
+// FRAG: A and W^T are fragment-packed (kr_frag_index), so every operand load
+// is one contiguous 1 KB read per wave; otherwise they are row-major and each
+// load gathers 16 rows x 64 bytes (about 3x slower).
+//
+// The MFMA is issued as W^T x A^T, i.e. the weight fragment in the A-operand
+// slot: the result lane then holds 4 consecutive output columns of one row,
+// so the epilogue reads and writes 8-byte (fp16) or 16-byte (fp32) vectors.
+// Every output element is still the same k-ordered chain of products.
+//
+// Workgroup -> tile: when a job has a multiple of 8 column groups, the
+// workgroups of one column group (which share its weight panels) all land on
+// the same XCD (workgroups are dealt to the 8 XCDs round robin), so each
+// weight byte is fetched into one L2.
+constexpr int kEpiPrefetch = 4;   // epilogue tiles per wave with prefetched res/gate
+
+template <int TM, int NS, bool FRAG, int MAXT>
+__global__ void __launch_bounds__(MAXT) gemm_panel_kernel(kr_gemm_multi mj) {
+    constexpr int TT = TM * NS;
+    extern __shared__ __attribute__((aligned(16))) float part_lds[];   // [S][TT][256]
     const int lane = threadIdx.x & 63, s = threadIdx.x >> 6;
     // Job of this workgroup; fields are copied with constant indices so every
     // kernel-argument load is issued up front (no dependent scalar loads).
     const int bid = blockIdx.x;
     const int j = bid < mj.tiles[0] ? 0 : (bid < mj.tiles[0] + mj.tiles[1] ? 1 : 2);
-    const int tile = bid - (j > 0 ? mj.tiles[0] : 0) - (j > 1 ? mj.tiles[1] : 0);
+    const int w = bid - (j > 0 ? mj.tiles[0] : 0) - (j > 1 ? mj.tiles[1] : 0);
     kr_gemm_args g;
     int ep;
     if (j == 0) { g = mj.job[0]; ep = mj.ep[0]; }
     else if (j == 1) { g = mj.job[1]; ep = mj.ep[1]; }
     else { g = mj.job[2]; ep = mj.ep[2]; }
     const int S = g.K / kKS;
-    const int ntn = (g.N + 16 * TN - 1) / (16 * TN);
-    const int m0 = (tile / ntn) * 16 * TM, n0 = (tile % ntn) * 16 * TN;
-    // Wave 0 applies the epilogue; fetch its residual / gate operands now so
-    // their latency overlaps the operand loads.
-    kr_half4 res_v[TM][TN], gate_v[TM][TN];
-    if (s == 0 && (ep == KR_EP_RESID || ep == KR_EP_GATED)) {
-        #pragma unroll
-        for (int i = 0; i < TM; i++)
-            #pragma unroll
-            for (int t = 0; t < TN; t++)
-                #pragma unroll
-                for (int r = 0; r < 4; r++) {
-                    const int m = min(m0 + 16 * i + (lane >> 4) * 4 + r, g.M - 1);
-                    const int n = min(n0 + 16 * t + (lane & 15), g.N - 1);
-                    const size_t o = (size_t)m * (size_t)g.ldo + (size_t)n;
-                    res_v[i][t][r] = g.res[o];
-                    gate_v[i][t][r] = ep == KR_EP_GATED ? g.gate[o] : (kr_half)0.0f;
-                }
+    const int mt = (g.M + 16 * TM - 1) / (16 * TM);
+    const int ng = (g.N + 16 * NS - 1) / (16 * NS);
+    int m_t, n_g;
+    if ((ng & 7) == 0) {
+        const int k = w >> 3;
+        n_g = (k / mt) * 8 + (w & 7);
+        m_t = k % mt;
+    } else {
+        m_t = w / ng;
+        n_g = w % ng;
     }
-    const int k0 = s * kKS + (lane >> 4) * 8;
-    kr_half8 a[TM][8], b[TN][8];
+    const int m0 = m_t * 16 * TM, n0 = n_g * 16 * NS;
+    const int last_mb = (g.M - 1) >> 4, last_nb = (g.N - 1) >> 4;
+
+    // ---- operand loads: A once, W panels double buffered
+    kr_half8 a[TM][8];
+    kr_half8 b[2][8];
+    const int kb = g.K >> 5;
+    auto load_w = [&](int t, kr_half8 (&dst)[8]) {
+        // panels beyond N re-read the last one; their outputs are never stored
+        if constexpr (FRAG) {
+            const int nb = min((n0 >> 4) + t, last_nb);
+            const kr_half* bp = g.Wf + ((size_t)nb * kb + 8 * s) * 512 + lane * 8;
+            #pragma unroll
+            for (int q = 0; q < 8; q++) dst[q] = *reinterpret_cast<const kr_half8*>(bp + 512 * q);
+        } else {
+            const int r = min(n0 + 16 * t + (lane & 15), g.N - 1);
+            const kr_half* bp = g.Wt + (size_t)r * g.ldw + s * kKS + (lane >> 4) * 8;
+            #pragma unroll
+            for (int q = 0; q < 8; q++) dst[q] = *reinterpret_cast<const kr_half8*>(bp + 32 * q);
+        }
+    };
     #pragma unroll
     for (int i = 0; i < TM; i++) {
-        // rows beyond M / N load a valid row; their outputs are never stored
-        const int r = min(m0 + 16 * i + (lane & 15), g.M - 1);
-        const kr_half* ap = g.A + (size_t)r * g.lda + k0;
-        #pragma unroll
-        for (int q = 0; q < 8; q++) a[i][q] = *reinterpret_cast<const kr_half8*>(ap + 32 * q);
+        if constexpr (FRAG) {
+            const int mb = min((m0 >> 4) + i, last_mb);
+            const kr_half* ap = g.A + ((size_t)mb * kb + 8 * s) * 512 + lane * 8;
+            #pragma unroll
+            for (int q = 0; q < 8; q++) a[i][q] = *reinterpret_cast<const kr_half8*>(ap + 512 * q);
+        } else {
+            const int r = min(m0 + 16 * i + (lane & 15), g.M - 1);
+            const kr_half* ap = g.A + (size_t)r * g.lda + s * kKS + (lane >> 4) * 8;
+            #pragma unroll
+            for (int q = 0; q < 8; q++) a[i][q] = *reinterpret_cast<const kr_half8*>(ap + 32 * q);
+        }
     }
-    #pragma unroll
-    for (int t = 0; t < TN; t++) {
-        const int r = min(n0 + 16 * t + (lane & 15), g.N - 1);
-        const kr_half* bp = g.Wt + (size_t)r * g.ldw + k0;
+    load_w(0, b[0]);
+    if constexpr (NS > 1) load_w(1, b[1]);
+
+    // ---- epilogue operands of this wave's tiles (t = s, s + S, ...), fetched
+    // behind the operand loads. The vector path needs 4-column groups that
+    // never straddle N and aligned pointers.
+    const bool has_res = ep == KR_EP_RESID || ep == KR_EP_GATED;
+    const uintptr_t ovec = ep == KR_EP_F32 ? 15 : 7;
+    const bool vec = g.out_frag ||
+                     ((g.N & 3) == 0 && (g.ldo & 3) == 0 && ((uintptr_t)g.out & ovec) == 0 &&
+                      (!has_res || ((uintptr_t)g.res & 7) == 0) &&
+                      (ep != KR_EP_GATED || ((uintptr_t)g.gate & 7) == 0));
+    const int my_tiles = s < TT ? (TT - 1 - s) / S + 1 : 0;
+    const bool prefetch = has_res && vec && my_tiles <= kEpiPrefetch;
+    kr_half4 res_v[kEpiPrefetch], gate_v[kEpiPrefetch];
+    auto tile_mn = [&](int t, int& m, int& nb) {
+        m = m0 + 16 * (t / NS) + (lane & 15);
+        nb = n0 + 16 * (t % NS) + 4 * (lane >> 4);
+    };
+    if (prefetch) {
+        const kr_half* gp = ep == KR_EP_GATED ? g.gate : g.res;
         #pragma unroll
-        for (int q = 0; q < 8; q++) b[t][q] = *reinterpret_cast<const kr_half8*>(bp + 32 * q);
+        for (int e = 0; e < kEpiPrefetch; e++) {
+            if (e < my_tiles) {
+                int m, nb;
+                tile_mn(s + e * S, m, nb);
+                const size_t o = (size_t)min(m, g.M - 1) * (size_t)g.ldo + (size_t)min(nb, g.N - 4);
+                res_v[e] = *reinterpret_cast<const kr_half4*>(g.res + o);
+                gate_v[e] = *reinterpret_cast<const kr_half4*>(gp + o);
+            }
+        }
     }
-    __builtin_amdgcn_sched_barrier(0);     // all loads in flight before the MFMAs
-    kr_float4 p[TM][TN];
+    __builtin_amdgcn_sched_barrier(0);     // loads in flight before the MFMAs
+
+    // ---- MFMA chains, one per (row block, panel)
+    kr_float4 p[TM][NS];
     #pragma unroll
-    for (int i = 0; i < TM; i++)
+    for (int t = 0; t < NS; t++) {
         #pragma unroll
-        for (int t = 0; t < TN; t++) {
+        for (int i = 0; i < TM; i++) {
             p[i][t] = kr_float4{0.f, 0.f, 0.f, 0.f};
             #pragma unroll
             for (int q = 0; q < 8; q++)
-                p[i][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[i][q], b[t][q], p[i][t], 0, 0, 0);
+                p[i][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(b[t & 1][q], a[i][q], p[i][t], 0, 0, 0);
         }
-    if (S > 1) {
-        if (s > 0) {
-            #pragma unroll
-            for (int i = 0; i < TM; i++)
-                #pragma unroll
-                for (int t = 0; t < TN; t++)
-                    *reinterpret_cast<kr_float4*>(
-                        part_lds + ((size_t)s * TM * TN + i * TN + t) * 256 + lane * 4) = p[i][t];
-        }
-        __syncthreads();
-        if (s != 0) return;
-        for (int q = 1; q < S; q++)
-            #pragma unroll
-            for (int i = 0; i < TM; i++)
-                #pragma unroll
-                for (int t = 0; t < TN; t++)
-                    p[i][t] = add4(p[i][t], *reinterpret_cast<const kr_float4*>(
-                        part_lds + ((size_t)q * TM * TN + i * TN + t) * 256 + lane * 4));
+        if (t + 2 < NS) load_w(t + 2, b[t & 1]);
     }
-    #pragma unroll
-    for (int i = 0; i < TM; i++)
-        #pragma unroll
-        for (int t = 0; t < TN; t++)
+
+    // ---- slice partials in LDS, then each tile summed in slice order
+    auto epilogue = [&](int t, int e, kr_float4 acc) {
+        int m, nb;
+        tile_mn(t, m, nb);
+        if (m >= g.M || nb >= g.N) return;
+        const size_t o = (size_t)m * (size_t)g.ldo + (size_t)nb;
+        if (vec) {
+            if (ep == KR_EP_F32) {
+                *reinterpret_cast<kr_float4*>(reinterpret_cast<float*>(g.out) + o) = acc;
+                return;
+            }
+            kr_half4 rv = kr_half4{0, 0, 0, 0}, gv = kr_half4{0, 0, 0, 0};
+            if (has_res) {
+                if (prefetch) {
+                    #pragma unroll
+                    for (int x = 0; x < kEpiPrefetch; x++)
+                        if (x == e) { rv = res_v[x]; gv = gate_v[x]; }
+                } else {
+                    rv = *reinterpret_cast<const kr_half4*>(g.res + o);
+                    if (ep == KR_EP_GATED) gv = *reinterpret_cast<const kr_half4*>(g.gate + o);
+                }
+            }
+            kr_half4 h;
             #pragma unroll
             for (int r = 0; r < 4; r++) {
-                const int m = m0 + 16 * i + (lane >> 4) * 4 + r;
-                const int n = n0 + 16 * t + (lane & 15);
-                if (m >= g.M || n >= g.N) continue;
-                const size_t o = (size_t)m * (size_t)g.ldo + (size_t)n;
-                const float acc = p[i][t][r];
-                if (ep == KR_EP_F32) {
-                    reinterpret_cast<float*>(g.out)[o] = acc;
-                    continue;
-                }
-                const float h = (float)(kr_half)acc;
+                const float x = (float)(kr_half)acc[r];
                 float y;
-                if (ep == KR_EP_F16) y = h;
-                else if (ep == KR_EP_SIGMOID) y = kr_sigmoid(h);
-                else if (ep == KR_EP_RELUSQ) { const float rr = h > 0.0f ? h : 0.0f; y = rr * rr; }
-                else if (ep == KR_EP_RESID) y = (float)res_v[i][t][r] + h;
-                else y = (float)res_v[i][t][r] + (float)(kr_half)((float)gate_v[i][t][r] * h);
-                reinterpret_cast<kr_half*>(g.out)[o] = (kr_half)y;
+                if (ep == KR_EP_F16) y = x;
+                else if (ep == KR_EP_SIGMOID) y = kr_sigmoid(x);
+                else if (ep == KR_EP_RELUSQ) { const float rr = x > 0.0f ? x : 0.0f; y = rr * rr; }
+                else if (ep == KR_EP_RESID) y = (float)rv[r] + x;
+                else y = (float)rv[r] + (float)(kr_half)((float)gv[r] * x);
+                h[r] = (kr_half)y;
             }
+            kr_half* dst = reinterpret_cast<kr_half*>(g.out) +
+                           (g.out_frag ? kr_frag_index(m, nb, g.N) : o);
+            *reinterpret_cast<kr_half4*>(dst) = h;
+        } else {
+            #pragma unroll
+            for (int r = 0; r < 4; r++)
+                if (nb + r < g.N) {
+                    switch (ep) {
+                        case KR_EP_F32: store_one<KR_EP_F32>(g, m, nb + r, acc[r]); break;
+                        case KR_EP_F16: store_one<KR_EP_F16>(g, m, nb + r, acc[r]); break;
+                        case KR_EP_SIGMOID: store_one<KR_EP_SIGMOID>(g, m, nb + r, acc[r]); break;
+                        case KR_EP_RELUSQ: store_one<KR_EP_RELUSQ>(g, m, nb + r, acc[r]); break;
+                        case KR_EP_RESID: store_one<KR_EP_RESID>(g, m, nb + r, acc[r]); break;
+                        default: store_one<KR_EP_GATED>(g, m, nb + r, acc[r]); break;
+                    }
+                }
+        }
+    };
+    if (S == 1) {
+        #pragma unroll
+        for (int t = 0; t < TT; t++) epilogue(t, t, p[t / NS][t % NS]);
+        return;
+    }
+    #pragma unroll
+    for (int t = 0; t < TT; t++)
+        *reinterpret_cast<kr_float4*>(part_lds + ((size_t)s * TT + t) * 256 + lane * 4) =
+            p[t / NS][t % NS];
+    __syncthreads();
+    for (int e = 0; e < my_tiles; e++) {
+        const int t = s + e * S;
+        kr_float4 acc = *reinterpret_cast<const kr_float4*>(part_lds + (size_t)t * 256 + lane * 4);
+        for (int q = 1; q < S; q++)
+            acc = add4(acc, *reinterpret_cast<const kr_float4*>(
+                                part_lds + ((size_t)q * TT + t) * 256 + lane * 4));
+        epilogue(t, e, acc);
+    }
 }
 
 template <int BM, int BN>
@@ -295,19 +395,87 @@ int launch_tile(const kr_gemm_args& g, int ep, hipStream_t s) {
     return KR_OK;
 }
 
-template <int TM, int TN>
-int launch_skinny(kr_gemm_multi mj, hipStream_t s) {
+struct PanelShape {
+    int TM, NS;
+};
+
+template <int TM, int NS, bool FRAG, int MAXT>
+int launch_panel(kr_gemm_multi mj, hipStream_t s) {
     const int S = mj.job[0].K / kKS;
     int total = 0;
     for (int j = 0; j < mj.njobs; j++) {
         const kr_gemm_args& g = mj.job[j];
-        mj.tiles[j] = ((g.M + 16 * TM - 1) / (16 * TM)) * ((g.N + 16 * TN - 1) / (16 * TN));
+        mj.tiles[j] = ((g.M + 16 * TM - 1) / (16 * TM)) * ((g.N + 16 * NS - 1) / (16 * NS));
         total += mj.tiles[j];
     }
-    const size_t lds = S > 1 ? (size_t)S * TM * TN * 256 * sizeof(float) : 0;
-    gemm_skinny_kernel<TM, TN><<<total, dim3(64 * S), lds, s>>>(mj);
+    const size_t lds = S > 1 ? (size_t)S * TM * NS * 256 * sizeof(float) : 0;
+    gemm_panel_kernel<TM, NS, FRAG, MAXT><<<total, dim3(64 * S), lds, s>>>(mj);
     KR_LAUNCHED();
     return KR_OK;
+}
+
+// Shapes compiled per block size: up to 12 slices TM {1, 2} x NS {1, 2};
+// up to 16 slices TM 1 x NS {1, 2}. Wider panels (NS > 2) cut the bytes a CU
+// reads but, with the registers a wave has, the third panel's loads wait for
+// the first panel's MFMAs: measured on MI355X at M = 256 they are 25-55%
+// slower, so every wave keeps all of its operand loads in flight at once.
+constexpr PanelShape kShapes256[] = {{1, 1}, {1, 2}, {2, 1}, {2, 2}};
+constexpr PanelShape kShapes768[] = {{1, 1}, {1, 2}, {2, 1}, {2, 2}};
+constexpr PanelShape kShapes1024[] = {{1, 1}, {1, 2}};
+
+// Busiest-CU operand bytes (in 128-byte lines) for a shape: workgroups are
+// spread over the 256 CUs, each reading (16*TM + 16*NS) x K halves; ties go
+// to the shape that occupies more CUs.
+long long panel_cost(const kr_gemm_multi& mj, PanelShape sh) {
+    long long wgs = 0;
+    for (int j = 0; j < mj.njobs; j++) {
+        const kr_gemm_args& g = mj.job[j];
+        wgs += (long long)((g.M + 16 * sh.TM - 1) / (16 * sh.TM)) *
+               ((g.N + 16 * sh.NS - 1) / (16 * sh.NS));
+    }
+    const long long per_wg = (long long)(sh.TM + sh.NS) * mj.job[0].K / 4;
+    return ((wgs + 255) / 256) * per_wg * 4096 - std::min<long long>(wgs, 256);
+}
+
+template <bool FRAG, int MAXT, size_t N>
+int launch_best(const kr_gemm_multi& mj, const PanelShape (&shapes)[N], hipStream_t s) {
+    PanelShape best = shapes[0];
+    long long best_cost = panel_cost(mj, best);
+    for (size_t i = 1; i < N; i++) {
+        const long long c = panel_cost(mj, shapes[i]);
+        if (c < best_cost) { best_cost = c; best = shapes[i]; }
+    }
+#define KR_PANEL(TM_, NS_) \
+    if (best.TM == TM_ && best.NS == NS_) return launch_panel<TM_, NS_, FRAG, MAXT>(mj, s);
+    if constexpr (MAXT == 256 || MAXT == 768) {
+        KR_PANEL(1, 1) KR_PANEL(1, 2) KR_PANEL(2, 1) KR_PANEL(2, 2)
+    } else {
+        KR_PANEL(1, 1) KR_PANEL(1, 2)
+    }
+#undef KR_PANEL
+    return kr_fail(KR_EINVAL, "gemm: no panel shape");
+}
+
+template <bool FRAG>
+int launch_small(const kr_gemm_multi& mj, hipStream_t s) {
+    const int S = mj.job[0].K / kKS;
+    if (S <= 4) return launch_best<FRAG, 256>(mj, kShapes256, s);
+    if (S <= 12) return launch_best<FRAG, 768>(mj, kShapes768, s);
+    return launch_best<FRAG, 1024>(mj, kShapes1024, s);
+}
+
+// Pack Wt [N, K] (row stride ld) into the fragment layout; rows N..N16-1 are zero.
+__global__ void pack_frag_kernel(const kr_half* __restrict__ Wt, long long ld, int N, int K,
+                                 kr_half* __restrict__ out) {
+    const long long N16 = kr_frag_rows(N);
+    const long long chunks = N16 * (K / 8);   // 8-half groups
+    for (long long c = (long long)blockIdx.x * blockDim.x + threadIdx.x; c < chunks;
+         c += (long long)gridDim.x * blockDim.x) {
+        const long long r = c / (K / 8), k = (c % (K / 8)) * 8;
+        kr_half8 v = kr_half8{0, 0, 0, 0, 0, 0, 0, 0};
+        if (r < N) v = *reinterpret_cast<const kr_half8*>(Wt + r * ld + k);
+        *reinterpret_cast<kr_half8*>(out + kr_frag_index(r, k, K)) = v;
+    }
 }
 
 // Transpose W [K, N] -> Wt [N, K] (rows of Wt beyond N are not touched).
@@ -327,20 +495,24 @@ __global__ void transpose_kernel(const kr_half* __restrict__ W, long long ldw_in
     }
 }
 
-constexpr int kSkinnyMaxM = 512;
 
 }  // namespace
 
 int check_args(const kr_gemm_args& g, int ep) {
-    KR_REQUIRE(g.A && g.Wt && g.out, "gemm: null pointer");
+    KR_REQUIRE(g.A && (g.Wt || g.Wf) && g.out, "gemm: null pointer");
     KR_REQUIRE(g.M >= 0 && g.N >= 1 && g.K >= kKS && g.K % kKS == 0,
                "gemm: unsupported shape M=%d N=%d K=%d (K must be a multiple of %d)", g.M, g.N,
                g.K, kKS);
-    KR_REQUIRE(g.lda % 8 == 0 && g.ldw % 8 == 0 && g.lda >= g.K && g.ldw >= g.K,
-               "gemm: lda/ldw must be >= K and multiples of 8");
-    KR_REQUIRE(((uintptr_t)g.A & 15) == 0 && ((uintptr_t)g.Wt & 15) == 0,
-               "gemm: A and Wt must be 16-byte aligned");
-    KR_REQUIRE(g.ldo >= g.N, "gemm: ldo < N");
+    KR_REQUIRE(g.a_frag || (g.lda % 8 == 0 && g.lda >= g.K), "gemm: lda must be >= K, multiple of 8");
+    KR_REQUIRE(!g.Wt || (g.ldw % 8 == 0 && g.ldw >= g.K), "gemm: ldw must be >= K, multiple of 8");
+    KR_REQUIRE(((uintptr_t)g.A & 15) == 0 && ((uintptr_t)g.Wt & 15) == 0 &&
+                   ((uintptr_t)g.Wf & 15) == 0,
+               "gemm: A, Wt and Wf must be 16-byte aligned");
+    KR_REQUIRE(g.out_frag || g.ldo >= g.N, "gemm: ldo < N");
+    KR_REQUIRE(!g.a_frag || g.Wf, "gemm: fragment-packed A needs fragment-packed W");
+    KR_REQUIRE(!g.out_frag || (g.N % 32 == 0 && ep != KR_EP_F32 && ep != KR_EP_RESID &&
+                               ep != KR_EP_GATED && ((uintptr_t)g.out & 7) == 0),
+               "gemm: fragment-packed output needs N %% 32 == 0 and an elementwise fp16 epilogue");
     KR_REQUIRE(ep >= KR_EP_F32 && ep <= KR_EP_GATED, "gemm: unknown epilogue %d", ep);
     KR_REQUIRE((ep != KR_EP_RESID && ep != KR_EP_GATED) || g.res, "gemm: residual missing");
     KR_REQUIRE(ep != KR_EP_GATED || g.gate, "gemm: gate missing");
@@ -354,22 +526,33 @@ int kr_gemm_launch_multi(const kr_gemm_args* jobs, const int* eps, int njobs, hi
         if (rc) return rc;
     }
     const int M = jobs[0].M, K = jobs[0].K;
-    bool same = true, small_n = true;
-    for (int j = 1; j < njobs; j++) same = same && jobs[j].M == M && jobs[j].K == K;
-    for (int j = 0; j < njobs; j++) small_n = small_n && jobs[j].N < 16384;
+    bool same = true, small_n = true, frag = jobs[0].a_frag != 0, any_frag = false;
+    for (int j = 1; j < njobs; j++)
+        same = same && jobs[j].M == M && jobs[j].K == K && (jobs[j].a_frag != 0) == frag;
+    for (int j = 0; j < njobs; j++) {
+        small_n = small_n && jobs[j].N < KR_GEMM_SMALL_MAX_N;
+        any_frag = any_frag || jobs[j].a_frag || jobs[j].out_frag;
+    }
     if (M == 0) return KR_OK;
-    if (M <= kSkinnyMaxM && same && small_n) {
-        KR_REQUIRE(K / kKS <= 12, "gemm: K=%d too large for the small-M path", K);
+    const bool small = M <= KR_GEMM_SMALL_M && same && small_n;
+    KR_REQUIRE(small || !any_frag, "gemm: fragment-packed operands need the small-M path "
+               "(M <= %d, N < %d, one M/K/layout per launch)", KR_GEMM_SMALL_M, KR_GEMM_SMALL_MAX_N);
+    if (small) {
+        KR_REQUIRE(K / kKS <= 16, "gemm: K=%d too large for the small-M path", K);
         kr_gemm_multi mj{};
         mj.njobs = njobs;
         for (int j = 0; j < njobs; j++) { mj.job[j] = jobs[j]; mj.ep[j] = eps[j]; }
-        return M >= 32 ? launch_skinny<2, 2>(mj, s) : launch_skinny<1, 2>(mj, s);
+        if (frag) return launch_small<true>(mj, s);
+        // row-major A: fragment weights are not used, the row-major copy must exist
+        for (int j = 0; j < njobs; j++) KR_REQUIRE(jobs[j].Wt, "gemm: row-major W missing");
+        return launch_small<false>(mj, s);
     }
     for (int j = 0; j < njobs; j++) {
         const kr_gemm_args& g = jobs[j];
+        KR_REQUIRE(g.Wt, "gemm: row-major W missing");
         int rc;
         if (g.M >= 4096) rc = launch_tile<128, 128>(g, eps[j], s);
-        else if (g.M > kSkinnyMaxM) rc = launch_tile<64, 64>(g, eps[j], s);
+        else if (g.M > KR_GEMM_SMALL_M) rc = launch_tile<64, 64>(g, eps[j], s);
         else rc = launch_tile<64, 128>(g, eps[j], s);   // small M, huge N (the head)
         if (rc) return rc;
     }
@@ -392,6 +575,22 @@ int kr_transpose_f16(const uint16_t* W, long long ldw, int K, int N, uint16_t* W
     return KR_OK;
 }
 
+size_t kr_fragment_bytes(int N, int K) {
+    if (N < 1 || K < 32 || K % 32) return 0;
+    return (size_t)kr_frag_rows(N) * (size_t)K * 2;
+}
+
+int kr_pack_fragments(const uint16_t* Wt, long long ld, int N, int K, uint16_t* out, void* stream) {
+    KR_REQUIRE(Wt && out && N >= 1 && K >= 32 && K % 32 == 0 && ld >= K && ld % 8 == 0,
+               "kr_pack_fragments: bad args (K must be a multiple of 32)");
+    KR_REQUIRE(((uintptr_t)Wt & 15) == 0 && ((uintptr_t)out & 15) == 0,
+               "kr_pack_fragments: pointers must be 16-byte aligned");
+    pack_frag_kernel<<<512, 256, 0, kr_stream(stream)>>>(reinterpret_cast<const kr_half*>(Wt), ld,
+                                                         N, K, reinterpret_cast<kr_half*>(out));
+    KR_LAUNCHED();
+    return KR_OK;
+}
+
 int kr_det_matmul(const uint16_t* x, int M, int K, const uint16_t* Wt, long long ldw, int N,
                   void* out, long long ldo, int epilogue, const uint16_t* res,
                   const uint16_t* gate, void* stream) {
@@ -407,6 +606,25 @@ int kr_det_matmul(const uint16_t* x, int M, int K, const uint16_t* Wt, long long
     g.M = M;
     g.N = N;
     g.K = K;
+    return kr_gemm_launch(g, epilogue, kr_stream(stream));
+}
+
+int kr_det_matmul_packed(const uint16_t* xf, int M, int K, const uint16_t* Wf, int N, void* out,
+                         long long ldo, int epilogue, const uint16_t* res, const uint16_t* gate,
+                         int out_packed, void* stream) {
+    kr_gemm_args g{};
+    g.A = reinterpret_cast<const kr_half*>(xf);
+    g.lda = K;
+    g.Wf = reinterpret_cast<const kr_half*>(Wf);
+    g.out = out;
+    g.ldo = ldo;
+    g.res = reinterpret_cast<const kr_half*>(res);
+    g.gate = reinterpret_cast<const kr_half*>(gate);
+    g.M = M;
+    g.N = N;
+    g.K = K;
+    g.a_frag = 1;
+    g.out_frag = out_packed ? 1 : 0;
     return kr_gemm_launch(g, epilogue, kr_stream(stream));
 }
 

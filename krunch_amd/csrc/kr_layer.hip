@@ -47,9 +47,28 @@ __device__ __forceinline__ float wave_sum(float s) {
     return s;
 }
 
+// Per-lane copies of a [C] fp16 coefficient vector (the lane's 4-column groups).
 template <int G>
-__device__ __forceinline__ void layer_norm_row(RowF<G>& r, const kr_half* __restrict__ w,
-                                               const kr_half* __restrict__ b, int lane) {
+struct CoefH {
+    kr_half4 v[G];
+};
+
+template <int G>
+__device__ __forceinline__ void load_coef(const kr_half* __restrict__ p, int lane, CoefH<G>& c) {
+    #pragma unroll
+    for (int i = 0; i < G; i++) c.v[i] = *reinterpret_cast<const kr_half4*>(p + 256 * i + 4 * lane);
+}
+
+template <int G>
+__device__ __forceinline__ void to_float(const CoefH<G>& h, RowF<G>& r) {
+    #pragma unroll
+    for (int i = 0; i < G; i++)
+        #pragma unroll
+        for (int q = 0; q < 4; q++) r.v[i][q] = (float)h.v[i][q];
+}
+
+template <int G>
+__device__ __forceinline__ void layer_norm_row(RowF<G>& r, const CoefH<G>& w, const CoefH<G>& b) {
     constexpr float invC = 1.0f / (float)(256 * G);
     float s = 0.0f;
     #pragma unroll
@@ -68,11 +87,9 @@ __device__ __forceinline__ void layer_norm_row(RowF<G>& r, const kr_half* __rest
     const float rstd = 1.0f / sqrtf(wave_sum(ss) * invC + kLnEps);
     #pragma unroll
     for (int i = 0; i < G; i++) {
-        const kr_half4 wh = *reinterpret_cast<const kr_half4*>(w + 256 * i + 4 * lane);
-        const kr_half4 bh = *reinterpret_cast<const kr_half4*>(b + 256 * i + 4 * lane);
         #pragma unroll
         for (int q = 0; q < 4; q++) {
-            const float y = (r.v[i][q] - mean) * rstd * (float)wh[q] + (float)bh[q];
+            const float y = (r.v[i][q] - mean) * rstd * (float)w.v[i][q] + (float)b.v[i][q];
             r.v[i][q] = (float)(kr_half)y;   // activations are fp16
         }
     }
@@ -89,20 +106,25 @@ __device__ __forceinline__ void store_row(kr_half* __restrict__ p, int lane, con
     }
 }
 
-// mix = fp16(xx * tm + sx * (1 - tm))   (premix_kernels.cu:19-54 semantics)
+// mix = fp16(xx * tm + sx * (1 - tm))   (premix_kernels.cu:19-54 semantics),
+// stored into row `row` of a row-major or fragment-packed [*, C] operand.
 template <int G>
-__device__ __forceinline__ void store_mix(kr_half* __restrict__ out, const kr_half* __restrict__ tm,
-                                          int lane, const RowF<G>& cur, const RowF<G>& prev) {
+__device__ __forceinline__ void store_mix(kr_half* __restrict__ out, size_t row, bool frag,
+                                          const CoefH<G>& tm, int lane,
+                                          const RowF<G>& cur, const RowF<G>& prev) {
+    constexpr int C = 256 * G;
     #pragma unroll
     for (int i = 0; i < G; i++) {
-        const kr_half4 t = *reinterpret_cast<const kr_half4*>(tm + 256 * i + 4 * lane);
+        const kr_half4 t = tm.v[i];
         kr_half4 h;
         #pragma unroll
         for (int q = 0; q < 4; q++) {
             const float m = (float)t[q];
             h[q] = (kr_half)(cur.v[i][q] * m + prev.v[i][q] * (1.0f - m));
         }
-        *reinterpret_cast<kr_half4*>(out + 256 * i + 4 * lane) = h;
+        const int col = 256 * i + 4 * lane;
+        const size_t o = frag ? kr_frag_index((long long)row, col, C) : row * C + col;
+        *reinterpret_cast<kr_half4*>(out + o) = h;
     }
 }
 
@@ -114,15 +136,19 @@ struct LnMixArgs {
     kr_half* out[3];           // NMIX outputs [B*T, C]
     kr_half* state;            // [B, C] shifted-in row for t = 0; rewritten with LN(x[T-1])
     int B, T, run;             // rows per wave
+    int frag;                  // mix outputs fragment-packed (small-M GEMM operands)
 };
 
 // One wave per run of `run` consecutive tokens of one stream. The wave that
 // owns t = 0 reads the carried state first and rewrites it last (with the
-// LayerNorm of row T-1), so no other wave touches the state.
+// LayerNorm of row T-1), so no other wave touches the state. Every
+// coefficient and the first rows are loaded before any store, so a T = 1
+// row costs one memory round trip.
 // NMIX == 0: plain LayerNorm into out[0] (ln_out before the head).
 template <int G, int NMIX>
 __global__ void __launch_bounds__(256) ln_mix_kernel(LnMixArgs a) {
     constexpr int C = 256 * G;
+    constexpr int NM = NMIX > 0 ? NMIX : 1;
     const int lane = threadIdx.x & 63;
     const int gw = (blockIdx.x * blockDim.x + threadIdx.x) >> 6;
     const int runs = (a.T + a.run - 1) / a.run;
@@ -131,24 +157,33 @@ __global__ void __launch_bounds__(256) ln_mix_kernel(LnMixArgs a) {
     const int t1 = min(a.T, t0 + a.run);
     const size_t row0 = (size_t)b * a.T;
 
+    CoefH<G> w, bias, tm[NM];
+    load_coef<G>(a.ln_w, lane, w);
+    load_coef<G>(a.ln_b, lane, bias);
+    if constexpr (NMIX > 0) {
+        #pragma unroll
+        for (int m = 0; m < NMIX; m++) load_coef<G>(a.tm[m], lane, tm[m]);
+    }
+    // the first row and the row shifted in ahead of it, both in flight at once
+    CoefH<G> prev_h, first_h;
+    if constexpr (NMIX > 0)
+        load_coef<G>(t0 == 0 ? a.state + (size_t)b * C : a.x + (row0 + t0 - 1) * C, lane, prev_h);
+    load_coef<G>(a.x + (row0 + t0) * C, lane, first_h);
     RowF<G> prev, cur;
     if constexpr (NMIX > 0) {
-        if (t0 == 0) {
-            load_row<G>(a.state + (size_t)b * C, lane, prev);
-        } else {
-            load_row<G>(a.x + (row0 + t0 - 1) * C, lane, prev);
-            layer_norm_row<G>(prev, a.ln_w, a.ln_b, lane);
-        }
+        to_float<G>(prev_h, prev);
+        if (t0 != 0) layer_norm_row<G>(prev, w, bias);
     }
     for (int t = t0; t < t1; t++) {
-        load_row<G>(a.x + (row0 + t) * C, lane, cur);
-        layer_norm_row<G>(cur, a.ln_w, a.ln_b, lane);
+        if (t == t0) to_float<G>(first_h, cur);
+        else load_row<G>(a.x + (row0 + t) * C, lane, cur);
+        layer_norm_row<G>(cur, w, bias);
         if constexpr (NMIX == 0) {
             store_row<G>(a.out[0] + (row0 + t) * C, lane, cur);
         } else {
             #pragma unroll
             for (int m = 0; m < NMIX; m++)
-                store_mix<G>(a.out[m] + (row0 + t) * C, a.tm[m], lane, cur, prev);
+                store_mix<G>(a.out[m], row0 + t, a.frag != 0, tm[m], lane, cur, prev);
             prev = cur;
         }
     }
@@ -156,7 +191,7 @@ __global__ void __launch_bounds__(256) ln_mix_kernel(LnMixArgs a) {
         if (t0 == 0) {
             if (t1 < a.T) {
                 load_row<G>(a.x + (row0 + a.T - 1) * C, lane, cur);
-                layer_norm_row<G>(cur, a.ln_w, a.ln_b, lane);
+                layer_norm_row<G>(cur, w, bias);
             }
             store_row<G>(a.state + (size_t)b * C, lane, cur);
         }
@@ -166,9 +201,31 @@ __global__ void __launch_bounds__(256) ln_mix_kernel(LnMixArgs a) {
 // ---------------------------------------------------------------------------
 // WKV recurrence (wkv_kernel.cu:52-73 semantics), one lane per (stream,
 // channel), sequential over T; fused with the receptance product:
-// ry = fp16(r * fp16(y)). State aa, bb, pp is read once and written once.
+// ry = fp16(r * fp16(y)), written row-major or fragment-packed (ry_frag) for
+// the output projection. State aa, bb, pp is read once and written once.
 // ---------------------------------------------------------------------------
 constexpr int kWkvChunk = 8;
+
+struct WkvState {
+    float a, b, p;
+};
+
+// One token of the recurrence; returns ry.
+__device__ __forceinline__ kr_half wkv_token(WkvState& st, float w, float u, float kk, float vv,
+                                             float rr) {
+    const float ww = u + kk;
+    const float p1 = fmaxf(st.p, ww);
+    const float e1 = __expf(st.p - p1), e2 = __expf(ww - p1);
+    const float y = (e1 * st.a + e2 * vv) / (e1 * st.b + e2);
+    const kr_half ry = (kr_half)(rr * (float)(kr_half)y);
+    const float ww2 = w + st.p;
+    const float p2 = fmaxf(ww2, kk);
+    const float f1 = __expf(ww2 - p2), f2 = __expf(kk - p2);
+    st.a = f1 * st.a + f2 * vv;
+    st.b = f1 * st.b + f2;
+    st.p = p2;
+    return ry;
+}
 
 __global__ void __launch_bounds__(256) wkv_kernel(const float* __restrict__ k,
                                                   const float* __restrict__ v,
@@ -177,15 +234,21 @@ __global__ void __launch_bounds__(256) wkv_kernel(const float* __restrict__ k,
                                                   const float* __restrict__ first,
                                                   float* __restrict__ aa, float* __restrict__ bb,
                                                   float* __restrict__ pp, kr_half* __restrict__ ry,
-                                                  int B, int T, int C) {
+                                                  int B, int T, int C, int ry_frag) {
     const int c = blockIdx.x * blockDim.x + threadIdx.x;
     const int b = blockIdx.y;
     if (c >= C || b >= B) return;
-    const float w = decay[c], u = first[c];
     const size_t s = (size_t)b * C + c;
-    float a_ = aa[s], b_ = bb[s], p_ = pp[s];
     const size_t base = (size_t)b * T * C + c;
-    for (int t0 = 0; t0 < T; t0 += kWkvChunk) {
+    // token 0 and every operand it needs are loaded together (T >= 1)
+    const float w = decay[c], u = first[c];
+    WkvState st{aa[s], bb[s], pp[s]};
+    const float k0 = k[base], v0 = v[base], r0 = (float)r[base];
+    auto ry_at = [&](int t) -> size_t {
+        return ry_frag ? kr_frag_index((long long)b * T + t, c, C) : base + (size_t)t * C;
+    };
+    ry[ry_at(0)] = wkv_token(st, w, u, k0, v0, r0);
+    for (int t0 = 1; t0 < T; t0 += kWkvChunk) {
         float kk[kWkvChunk], vv[kWkvChunk], rr[kWkvChunk];
         #pragma unroll
         for (int q = 0; q < kWkvChunk; q++) {
@@ -197,25 +260,12 @@ __global__ void __launch_bounds__(256) wkv_kernel(const float* __restrict__ k,
             }
         }
         #pragma unroll
-        for (int q = 0; q < kWkvChunk; q++) {
-            if (t0 + q < T) {
-                const float ww = u + kk[q];
-                const float p1 = fmaxf(p_, ww);
-                const float e1 = __expf(p_ - p1), e2 = __expf(ww - p1);
-                const float y = (e1 * a_ + e2 * vv[q]) / (e1 * b_ + e2);
-                ry[base + (size_t)(t0 + q) * C] = (kr_half)(rr[q] * (float)(kr_half)y);
-                const float ww2 = w + p_;
-                const float p2 = fmaxf(ww2, kk[q]);
-                const float f1 = __expf(ww2 - p2), f2 = __expf(kk[q] - p2);
-                a_ = f1 * a_ + f2 * vv[q];
-                b_ = f1 * b_ + f2;
-                p_ = p2;
-            }
-        }
+        for (int q = 0; q < kWkvChunk; q++)
+            if (t0 + q < T) ry[ry_at(t0 + q)] = wkv_token(st, w, u, kk[q], vv[q], rr[q]);
     }
-    aa[s] = a_;
-    bb[s] = b_;
-    pp[s] = p_;
+    aa[s] = st.a;
+    bb[s] = st.b;
+    pp[s] = st.p;
 }
 
 // x[row] = emb[ids[row]] (ids clamped into [0, V) so a bad id cannot read
@@ -285,12 +335,15 @@ struct Work {
 
 inline size_t up256(size_t b) { return (b + 255) / 256 * 256; }
 
+// Buffers hold M rounded up to 16 rows so fragment-packed operands are whole blocks.
 size_t work_bytes(long long M, int C, int F) {
+    M = kr_frag_rows(M);
     const size_t h = (size_t)M * C * 2, f = (size_t)M * C * 4, kf = (size_t)M * F * 2;
     return 8 * up256(h) + 2 * up256(f) + up256(kf);
 }
 
 Work carve(void* ws, long long M, int C, int F) {
+    M = kr_frag_rows(M);
     char* p = static_cast<char*>(ws);
     auto take = [&](size_t bytes) { char* q = p; p += up256(bytes); return q; };
     const size_t h = (size_t)M * C * 2, f = (size_t)M * C * 4;
@@ -312,8 +365,12 @@ Work carve(void* ws, long long M, int C, int F) {
 int rows_per_run(int T) { return T >= 64 ? 16 : (T >= 8 ? 4 : 1); }
 
 kr_gemm_args gemm_args(const kr_half* A, int M, int K, const void* Wt, int N, void* out,
-                       const kr_half* res = nullptr, const kr_half* gate = nullptr) {
+                       const kr_half* res = nullptr, const kr_half* gate = nullptr,
+                       const void* Wf = nullptr, bool a_frag = false, bool out_frag = false) {
     kr_gemm_args g{};
+    g.Wf = H(Wf);
+    g.a_frag = a_frag ? 1 : 0;
+    g.out_frag = out_frag ? 1 : 0;
     g.A = A;
     g.lda = K;
     g.Wt = H(Wt);
@@ -334,9 +391,16 @@ kr_gemm_args gemm_args(const kr_half* A, int M, int K, const void* Wt, int N, vo
         if (kr_rc_) return kr_rc_; \
     } while (0)
 
+// Small-M calls (the stepped decode) keep every GEMM operand fragment-packed:
+// the LN-mix, WKV and ReLU^2 producers write that layout directly.
+bool use_fragments(const kr_layer_weights& L, long long M) {
+    return M <= KR_GEMM_SMALL_M && L.Kf && L.Vf && L.Rf && L.Of && L.fKf && L.fVf && L.fRf;
+}
+
 int layer_forward(const kr_layer_weights& L, int C, int F, kr_half* x, int B, int T,
                   const kr_layer_state& st, const Work& w, hipStream_t s) {
     const int M = B * T, G = C / 256;
+    const bool fr = use_fragments(L, M);
     LnMixArgs a{};
     a.x = x;
     a.ln_w = H(L.ln1_w);
@@ -347,21 +411,23 @@ int layer_forward(const kr_layer_weights& L, int C, int F, kr_half* x, int B, in
     a.B = B;
     a.T = T;
     a.run = rows_per_run(T);
+    a.frag = fr ? 1 : 0;
     KR_TRY(launch_ln_mix<3>(G, a, s));
     {
-        const kr_gemm_args jobs[3] = {gemm_args(w.kx, M, C, L.Kt, C, w.k),
-                                      gemm_args(w.vx, M, C, L.Vt, C, w.v),
-                                      gemm_args(w.rx, M, C, L.Rt, C, w.r)};
+        const kr_gemm_args jobs[3] = {
+            gemm_args(w.kx, M, C, L.Kt, C, w.k, nullptr, nullptr, L.Kf, fr),
+            gemm_args(w.vx, M, C, L.Vt, C, w.v, nullptr, nullptr, L.Vf, fr),
+            gemm_args(w.rx, M, C, L.Rt, C, w.r, nullptr, nullptr, L.Rf, fr)};
         const int eps[3] = {KR_EP_F32, KR_EP_F32, KR_EP_SIGMOID};
         KR_TRY(kr_gemm_launch_multi(jobs, eps, 3, s));
     }
     {
         dim3 grid((C + 255) / 256, B);
         wkv_kernel<<<grid, 256, 0, s>>>(w.k, w.v, w.r, L.decay, L.first, st.aa, st.bb, st.pp,
-                                        w.ry, B, T, C);
+                                        w.ry, B, T, C, fr ? 1 : 0);
         KR_LAUNCHED();
     }
-    KR_TRY(kr_gemm_launch(gemm_args(w.ry, M, C, L.Ot, C, x, x), KR_EP_RESID, s));
+    KR_TRY(kr_gemm_launch(gemm_args(w.ry, M, C, L.Ot, C, x, x, nullptr, L.Of, fr), KR_EP_RESID, s));
     a.ln_w = H(L.ln2_w);
     a.ln_b = H(L.ln2_b);
     a.tm[0] = H(L.ftm_k); a.tm[1] = H(L.ftm_r);
@@ -369,12 +435,13 @@ int layer_forward(const kr_layer_weights& L, int C, int F, kr_half* x, int B, in
     a.state = Hm(st.ffn_xx);
     KR_TRY(launch_ln_mix<2>(G, a, s));
     {
-        const kr_gemm_args jobs[2] = {gemm_args(w.frx, M, C, L.fRt, C, w.rf),
-                                      gemm_args(w.fkx, M, C, L.fKt, F, w.kf)};
+        const kr_gemm_args jobs[2] = {
+            gemm_args(w.frx, M, C, L.fRt, C, w.rf, nullptr, nullptr, L.fRf, fr),
+            gemm_args(w.fkx, M, C, L.fKt, F, w.kf, nullptr, nullptr, L.fKf, fr, fr)};
         const int eps[2] = {KR_EP_SIGMOID, KR_EP_RELUSQ};
         KR_TRY(kr_gemm_launch_multi(jobs, eps, 2, s));
     }
-    KR_TRY(kr_gemm_launch(gemm_args(w.kf, M, F, L.fVt, C, x, x, w.rf), KR_EP_GATED, s));
+    KR_TRY(kr_gemm_launch(gemm_args(w.kf, M, F, L.fVt, C, x, x, w.rf, L.fVf, fr), KR_EP_GATED, s));
     return KR_OK;
 }
 
@@ -532,7 +599,7 @@ int kr_wkv(int B, int T, int C, const float* decay, const float* first, const fl
     dim3 grid((C + 255) / 256, B);
     wkv_kernel<<<grid, 256, 0, kr_stream(stream)>>>(k, v, reinterpret_cast<const kr_half*>(r),
                                                     decay, first, aa, bb, pp,
-                                                    reinterpret_cast<kr_half*>(ry), B, T, C);
+                                                    reinterpret_cast<kr_half*>(ry), B, T, C, 0);
     KR_LAUNCHED();
     return KR_OK;
 }

@@ -4,8 +4,9 @@ recurrent-state buffer.
 `prepare(w)` takes a weight dict in the layout the reference reads
 (`krunch/cpp_path.py:59-86`: rwkv-package keys, matrices [in, out], raw
 `time_decay`) and builds, on the GPU, the copies the kernels want:
-matrices transposed to [out, in] (K contiguous, the MFMA operand layout),
-fp16 activations/weights, fp32 w = -exp(time_decay) and u = time_first.
+matrices transposed to [out, in] (K contiguous) plus a fragment-packed copy
+of each layer matrix (16 x 32 MFMA operand blocks, 1 KB contiguous each) for
+the small-M decode GEMMs, fp16 activations/weights, fp32 w = -exp(time_decay) and u = time_first.
 Tensor allocation is torch's; every transform is a HIP kernel of the library.
 
 `State` is one contiguous buffer holding all layers' recurrent state for B
@@ -28,6 +29,15 @@ MAT_KEYS_ATT = ("key", "value", "receptance", "output")
 
 def _dev(device):
     return torch.device(device if device is not None else "cuda")
+
+
+def _fragments(Wt: torch.Tensor) -> torch.Tensor:
+    """Fragment-packed copy of Wt [N, K] (kr_pack_fragments) for the small-M GEMM."""
+    N, K = Wt.shape
+    nbytes = _lib.lib().kr_fragment_bytes(N, K)
+    out = torch.empty(nbytes // 2, dtype=torch.float16, device=Wt.device)
+    _lib.call("kr_pack_fragments", Wt.data_ptr(), K, N, K, out.data_ptr(), _lib.stream_ptr())
+    return out
 
 
 def _transposed(W: torch.Tensor, device) -> torch.Tensor:
@@ -87,6 +97,8 @@ def prepare(w: dict, device=None) -> Prepared:
         L["fKt"] = _transposed(w[f + "key.weight"], device)
         L["fVt"] = _transposed(w[f + "value.weight"], device)
         L["fRt"] = _transposed(w[f + "receptance.weight"], device)
+        for src in ("K", "V", "R", "O", "fK", "fV", "fR"):
+            L[src + "f"] = _fragments(L[src + "t"])
         for name, tensor in L.items():
             t[f"{i}.{name}"] = tensor
             setattr(layers[i], name, tensor.data_ptr())

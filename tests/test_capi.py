@@ -29,7 +29,7 @@ def test_size_queries_without_device():
     L = _lib.lib()
     assert L.kr_state_bytes(12, 1, 768) == 147456          # 12 layers x 12288 B/stream
     assert L.kr_forward_workspace_bytes(1024, 768, 3072) >= 1024 * 768 * (8 * 2 + 2 * 4) + 1024 * 3072 * 2
-    assert L.kr_abi_version() == 1
+    assert L.kr_abi_version() == 2
 
 
 def test_argument_errors_are_reported():

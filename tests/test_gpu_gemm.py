@@ -68,3 +68,39 @@ def test_epilogues():
                                rtol=0, atol=2e-3)
     want = (res.float() + (gate.float() * h).half().float()).half().float()
     torch.testing.assert_close(_run(5, x, Wt, N, res=res, gate=gate).float(), want, rtol=0, atol=2e-3)
+
+
+@pytest.mark.parametrize("M,K,N,ep", [(256, 3072, 768, 5), (37, 768, 3072, 3), (5, 768, 768, 0),
+                                      (256, 768, 768, 4), (64, 768, 2304, 2)])
+def test_packed_operands_match_row_major(M, K, N, ep):
+    """kr_det_matmul_packed on fragment-packed x and W gives kr_det_matmul's
+    bits; with out_packed the fp16 result is the packed layout of the same."""
+    from krunch_amd import _lib
+    x, W = _mk(M, K, N, 11)
+    Wt = W.t().contiguous()
+    g = torch.Generator(device="cpu").manual_seed(12)
+    res = torch.randn((M, N), generator=g).half().cuda()
+    gate = torch.rand((M, N), generator=g).half().cuda()
+    want = _run(ep, x, Wt, N, res.clone(), gate)
+
+    def pack(X):
+        R, KK = X.shape
+        buf = torch.empty(_lib.lib().kr_fragment_bytes(R, KK) // 2, dtype=torch.float16,
+                          device="cuda")
+        _lib.call("kr_pack_fragments", X.data_ptr(), KK, R, KK, buf.data_ptr(), _lib.stream_ptr())
+        return buf
+
+    xf, Wf = pack(x), pack(Wt)
+    out = torch.empty_like(want)
+    r2 = res.clone()
+    if ep in (4, 5):
+        out = r2
+    _lib.call("kr_det_matmul_packed", xf.data_ptr(), M, K, Wf.data_ptr(), N, out.data_ptr(), N, ep,
+              r2.data_ptr(), gate.data_ptr(), 0, _lib.stream_ptr())
+    assert torch.equal(out, want)
+    if ep in (1, 2, 3):
+        of = torch.zeros(_lib.lib().kr_fragment_bytes(M, N) // 2, dtype=torch.float16,
+                         device="cuda")
+        _lib.call("kr_det_matmul_packed", xf.data_ptr(), M, K, Wf.data_ptr(), N, of.data_ptr(), N,
+                  ep, None, None, 1, _lib.stream_ptr())
+        assert torch.equal(of, pack(want))
