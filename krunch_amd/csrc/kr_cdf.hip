@@ -75,6 +75,8 @@ struct RowShared {
     float total;
     int amax, deficit, amax_leaf, hit_leaf, hit_start, hit_len;
     uint32_t target, hit_prefix;
+    kr_rc_state dstate;       // decoder state (decode mode)
+    kr_bit_window win;        // stream bits of this step (decode mode)
 };
 
 __device__ __forceinline__ float wave_max(float v) {
@@ -90,24 +92,48 @@ __device__ __forceinline__ bool better(float pv, int pi, float bv, int bi) {
     return pv > bv || (pv == bv && pi < bi);
 }
 
+// fp16 logits rows are first copied into LDS with 16-byte loads (element i
+// at stage[i + pad], pad making the copied chunks 16-byte aligned), then read
+// in the scattered leaf layout from there: the leaf layout read straight from
+// global memory requests every cache line about ten times.
+constexpr int kStageMax = 65536 + 16;
+
 template <int IN>
-__device__ __forceinline__ float load_val(const void* row, int i) {
-    if constexpr (IN == IN_LOGITS_F16) return (float)reinterpret_cast<const kr_half*>(row)[i];
+__device__ __forceinline__ float load_val(const void* row, const kr_half* stage, int pad, int i) {
+    if constexpr (IN == IN_LOGITS_F16) return (float)stage[pad + i];
     else return reinterpret_cast<const float*>(row)[i];
+}
+
+// Copy V fp16 values at rp (2-byte aligned) into stage[pad ..], pad in [0, 8).
+__device__ __forceinline__ int stage_row(const kr_half* __restrict__ rp, int V, kr_half* stage,
+                                         int tid) {
+    const int head = min((int)(((16 - ((uintptr_t)rp & 15)) & 15) >> 1), V);
+    const int pad = (8 - head) & 7;
+    const int nchunks = (V - head) / 8;
+    for (int c = tid; c < nchunks; c += kThreads)
+        *reinterpret_cast<kr_half8*>(stage + pad + head + 8 * c) =
+            *reinterpret_cast<const kr_half8*>(rp + head + 8 * c);
+    const int tail0 = head + 8 * nchunks;
+    if (tid < head) stage[pad + tid] = rp[tid];
+    if (tid >= 8 && tid - 8 < V - tail0) stage[pad + tail0 + tid - 8] = rp[tail0 + tid - 8];
+    return pad;
 }
 
 // Sum of all held values in numpy's order (see file header). Every thread
 // returns the same value.
-__device__ float row_sum_numpy(float (&v)[kMaxIt][17], const int (&nfull)[kMaxIt],
-                               const int (&rem)[kMaxIt], const int (&len)[kMaxIt],
+__device__ __forceinline__ int leaf_full(int len) { return len >= 8 ? (len >> 3) : 0; }
+__device__ __forceinline__ int leaf_rem(int len) { return len >= 8 ? (len & 7) : len; }
+
+__device__ float row_sum_numpy(float (&v)[kMaxIt][17], const int (&len)[kMaxIt],
                                const PlanArgs& P, RowShared& sh, int lane, int wave) {
     const int grp = lane >> 3, j = lane & 7;
     #pragma unroll
     for (int it = 0; it < kMaxIt; it++) {
+        const int nf = leaf_full(len[it]), rm = leaf_rem(len[it]);
         float r = v[it][0];
         #pragma unroll
         for (int k = 1; k < 16; k++)
-            if (k < nfull[it]) r = r + v[it][k];
+            if (k < nf) r = r + v[it][k];
         r = r + __shfl_xor(r, 1);
         r = r + __shfl_xor(r, 2);
         r = r + __shfl_xor(r, 4);
@@ -115,7 +141,7 @@ __device__ float row_sum_numpy(float (&v)[kMaxIt][17], const int (&nfull)[kMaxIt
         #pragma unroll
         for (int t = 0; t < 7; t++) {
             const float tv = __shfl(v[it][16], (grp << 3) + t);
-            if (t < rem[it]) res = res + tv;
+            if (t < rm) res = res + tv;
         }
         const int L = it * kLeavesPerIt + wave * 8 + grp;
         if (j == 0 && L < P.n_leaves) sh.node[L] = res;
@@ -144,18 +170,26 @@ row_cdf_kernel(const void* __restrict__ input, long long ld, int n_rows, PlanArg
                void* __restrict__ out, long long out_ld, const int32_t* __restrict__ symbols,
                DecodeArgs D) {
     __shared__ RowShared sh;
+    __shared__ __attribute__((aligned(16))) kr_half stage[IN == IN_LOGITS_F16 ? kStageMax : 8];
     const int row = blockIdx.x;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int grp = lane >> 3, j = lane & 7;
     const int V = P.V;
 
+    // Decoder state and the stream bits this step will consume, fetched by
+    // lane 0 up front so their latency overlaps the softmax.
+    kr_rc_state dst{};
+    kr_bit_window win{};
     if constexpr (MODE == M_DECODE) {
+        static_assert(IN == IN_LOGITS_F16, "decode reads fp16 logits");
         // Finished streams do nothing this step (uniform per workgroup).
         if (D.n_tokens && D.tok_count && D.tok_count[row] >= D.n_tokens[row]) return;
         if (tid == 0) {
-            const kr_rc_state st = D.states[row];
-            sh.target = kr_rc_target(st.low, st.high, st.pending_or_value, prec);
-            sh.hit_leaf = -1;
+            dst = D.states[row];
+            const uint32_t o = D.base ? (uint32_t)D.base[row] : 0u;
+            uint32_t lim = D.in_len > o ? D.in_len - o : 0u;
+            if (D.limits && (uint32_t)D.limits[row] < lim) lim = (uint32_t)D.limits[row];
+            win.open(D.in + (o < D.in_len ? o : 0u), lim, dst.bit_offset);
         }
     }
 
@@ -165,9 +199,23 @@ row_cdf_kernel(const void* __restrict__ input, long long ld, int n_rows, PlanArg
     else
         rowp = reinterpret_cast<const char*>(input) + (size_t)row * (size_t)ld * 4;
 
+    int pad = 0;
+    if constexpr (IN == IN_LOGITS_F16) {
+        pad = stage_row(reinterpret_cast<const kr_half*>(rowp), V, stage, tid);
+        if constexpr (MODE == M_DECODE) {
+            if (tid == 0) {   // parked in LDS until the symbol is known
+                sh.dstate = dst;
+                sh.win = win;
+                sh.target = kr_rc_target(dst.low, dst.high, dst.pending_or_value, prec);
+                sh.hit_leaf = -1;
+            }
+        }
+        __syncthreads();
+    }
+
     // ---- gather the row into registers, leaf layout ----
     float v[kMaxIt][17];
-    int start[kMaxIt], len[kMaxIt], nfull[kMaxIt], rem[kMaxIt];
+    int start[kMaxIt], len[kMaxIt];
     #pragma unroll
     for (int it = 0; it < kMaxIt; it++) {
         const int L = it * kLeavesPerIt + wave * 8 + grp;
@@ -175,18 +223,17 @@ row_cdf_kernel(const void* __restrict__ input, long long ld, int n_rows, PlanArg
         if (L < P.n_leaves) lf = P.leaves[L];
         start[it] = lf.x;
         len[it] = lf.y;
-        nfull[it] = lf.y >= 8 ? (lf.y >> 3) : 0;
-        rem[it] = lf.y >= 8 ? (lf.y & 7) : lf.y;
+        const int nf = leaf_full(lf.y), rm = leaf_rem(lf.y);
         #pragma unroll
         for (int k = 0; k < 16; k++)
-            v[it][k] = k < nfull[it] ? load_val<IN>(rowp, lf.x + j + 8 * k) : -INFINITY;
-        v[it][16] = j < rem[it] ? load_val<IN>(rowp, lf.x + 8 * nfull[it] + j) : -INFINITY;
+            v[it][k] = k < nf ? load_val<IN>(rowp, stage, pad, lf.x + j + 8 * k) : -INFINITY;
+        v[it][16] = j < rm ? load_val<IN>(rowp, stage, pad, lf.x + 8 * nf + j) : -INFINITY;
     }
 
     float inv_S = 1.0f;
+    float m = -INFINITY;
     if constexpr (IN == IN_LOGITS_F16) {
         // ---- row max (exact, order-free) ----
-        float m = -INFINITY;
         #pragma unroll
         for (int it = 0; it < kMaxIt; it++)
             #pragma unroll
@@ -202,7 +249,7 @@ row_cdf_kernel(const void* __restrict__ input, long long ld, int n_rows, PlanArg
         for (int it = 0; it < kMaxIt; it++)
             #pragma unroll
             for (int k = 0; k < 17; k++) v[it][k] = kr_kexp(__fsub_rn(v[it][k], m));
-        const float S = row_sum_numpy(v, nfull, rem, len, P, sh, lane, wave);
+        const float S = row_sum_numpy(v, len, P, sh, lane, wave);
         inv_S = 1.0f / S;
         #pragma unroll
         for (int it = 0; it < kMaxIt; it++)
@@ -219,16 +266,17 @@ row_cdf_kernel(const void* __restrict__ input, long long ld, int n_rows, PlanArg
         float* o = reinterpret_cast<float*>(out) + (size_t)row * (size_t)out_ld;
         #pragma unroll
         for (int it = 0; it < kMaxIt; it++) {
+            const int nf = leaf_full(len[it]), rm = leaf_rem(len[it]);
             #pragma unroll
             for (int k = 0; k < 16; k++)
-                if (k < nfull[it]) o[start[it] + j + 8 * k] = v[it][k];
-            if (j < rem[it]) o[start[it] + 8 * nfull[it] + j] = v[it][16];
+                if (k < nf) o[start[it] + j + 8 * k] = v[it][k];
+            if (j < rm) o[start[it] + 8 * nf + j] = v[it][16];
         }
         return;
     }
 
     // ---- cdf.py: p = q / max(sum(q), 1e-30) ----
-    const float P_sum = row_sum_numpy(v, nfull, rem, len, P, sh, lane, wave);
+    const float P_sum = row_sum_numpy(v, len, P, sh, lane, wave);
     const float denom = fmaxf(P_sum, 1e-30f);
     const float scale = (float)((1 << prec) - V);
 
@@ -245,11 +293,12 @@ row_cdf_kernel(const void* __restrict__ input, long long ld, int n_rows, PlanArg
     #pragma unroll
     for (int it = 0; it < kMaxIt; it++) {
         const int L = it * kLeavesPerIt + wave * 8 + grp;
+        const int nf = leaf_full(len[it]), rm = leaf_rem(len[it]);
         int lsum = 0;
         #pragma unroll
         for (int k = 0; k < 17; k++) {
-            const bool live = k < 16 ? (k < nfull[it]) : (j < rem[it]);
-            const int idx = k < 16 ? start[it] + j + 8 * k : start[it] + 8 * nfull[it] + j;
+            const bool live = k < 16 ? (k < nf) : (j < rm);
+            const int idx = k < 16 ? start[it] + j + 8 * k : start[it] + 8 * nf + j;
             const float p = v[it][k] / denom;
             const int c = (int)floorf(__fmul_rn(p, scale)) + 1;
             if (live) {
@@ -262,7 +311,6 @@ row_cdf_kernel(const void* __restrict__ input, long long ld, int n_rows, PlanArg
                     if (idx == sym) csym = c;
                 }
             }
-            if constexpr (MODE == M_DECODE) v[it][k] = __int_as_float(live ? c : 0);
         }
         if constexpr (MODE == M_DECODE) {
             lsum += __shfl_xor(lsum, 1);
@@ -377,16 +425,22 @@ row_cdf_kernel(const void* __restrict__ input, long long ld, int n_rows, PlanArg
         __syncthreads();
         const int Lstar = sh.hit_leaf;
         const int gi = sh.amax, deficit = sh.deficit;
+        // The owning lanes recompute the hit leaf's counts from the staged
+        // logits (same operations, same bits) instead of keeping every count.
         #pragma unroll
         for (int it = 0; it < kMaxIt; it++) {
             const int L = it * kLeavesPerIt + wave * 8 + grp;
             if (L == Lstar) {
+                const int nf = leaf_full(len[it]), rm = leaf_rem(len[it]);
                 #pragma unroll
                 for (int k = 0; k < 17; k++) {
-                    const bool live = k < 16 ? (k < nfull[it]) : (j < rem[it]);
-                    const int off = k < 16 ? j + 8 * k : 8 * nfull[it] + j;
+                    const bool live = k < 16 ? (k < nf) : (j < rm);
+                    const int off = k < 16 ? j + 8 * k : 8 * nf + j;
                     if (live) {
-                        const int c = __float_as_int(v[it][k]);
+                        const float x = load_val<IN>(rowp, stage, pad, start[it] + off);
+                        const float q = __fmul_rn(kr_kexp(__fsub_rn(x, m)), inv_S);
+                        const float p = q / denom;
+                        const int c = (int)floorf(__fmul_rn(p, scale)) + 1;
                         sh.leaf_buf[off] = c + (start[it] + off == gi ? deficit : 0);
                     }
                 }
@@ -394,36 +448,49 @@ row_cdf_kernel(const void* __restrict__ input, long long ld, int n_rows, PlanArg
             }
         }
         __syncthreads();
-        if (tid == 0) {
-            // A valid CDF always contains the target; the guard keeps a
-            // corrupt stream from reading unset LDS.
+        if (wave == 0) {
+            // Symbol search inside the hit leaf (<= 128 counts): two counts
+            // per lane, an inclusive scan, and the first lane whose range
+            // holds the target. A valid CDF always contains the target; the
+            // guard keeps a corrupt stream from reading unset LDS.
             const bool hit = Lstar >= 0;
             const int s0 = hit ? sh.hit_start : V - 1, n = hit ? sh.hit_len : 0;
-            uint32_t run = hit ? sh.hit_prefix : (1u << prec) - 1u;
-            int s = hit ? s0 + n - 1 : V - 1;
-            uint32_t clo = run, chi = hit ? run : (1u << prec);
-            for (int i = 0; i < n; i++) {
-                const uint32_t c = (uint32_t)sh.leaf_buf[i];
-                if (target < run + c) { s = s0 + i; clo = run; chi = run + c; break; }
-                run += c;
+            const uint32_t base_run = hit ? sh.hit_prefix : (1u << prec) - 1u;
+            const uint32_t c0 = 2 * lane < n ? (uint32_t)sh.leaf_buf[2 * lane] : 0u;
+            const uint32_t c1 = 2 * lane + 1 < n ? (uint32_t)sh.leaf_buf[2 * lane + 1] : 0u;
+            uint32_t incl = c0 + c1;
+            for (int o = 1; o < 64; o <<= 1) {
+                const uint32_t up = __shfl_up(incl, o);
+                if (lane >= o) incl += up;
             }
-            kr_rc_state st = D.states[row];
-            kr_bit_source src;
-            const uint32_t o = D.base ? (uint32_t)D.base[row] : 0u;
-            uint32_t lim = D.in_len > o ? D.in_len - o : 0u;
-            if (D.limits && (uint32_t)D.limits[row] < lim) lim = (uint32_t)D.limits[row];
-            src.buf = D.in + (o < D.in_len ? o : 0u);
-            src.limit = lim;
-            src.pos = st.bit_offset;
-            kr_rc_consume(st.low, st.high, st.pending_or_value, clo, chi, prec, src);
-            st.bit_offset = src.pos;
-            D.states[row] = st;
-            D.out_syms[row] = s;
-            if (D.tokens) {
-                const int cnt = D.tok_count ? D.tok_count[row] : 0;
-                if (cnt >= 0 && cnt < D.tok_stride)
-                    D.tokens[(size_t)row * (size_t)D.tok_stride + cnt] = s;
-                if (D.tok_count) D.tok_count[row] = cnt + 1;
+            const uint32_t run0 = base_run + incl - (c0 + c1);   // before this lane's pair
+            const bool h0 = 2 * lane < n && target < run0 + c0;
+            const bool h1 = 2 * lane + 1 < n && !h0 && target < run0 + c0 + c1;
+            const unsigned long long ball = __ballot(h0 || h1);
+            const int src_lane = ball ? __ffsll(ball) - 1 : 0;
+            const int s_l = h0 ? s0 + 2 * lane : s0 + 2 * lane + 1;
+            const uint32_t lo_l = h0 ? run0 : run0 + c0;
+            const uint32_t hi_l = h0 ? run0 + c0 : run0 + c0 + c1;
+            int s = __shfl(s_l, src_lane);
+            uint32_t clo = __shfl(lo_l, src_lane), chi = __shfl(hi_l, src_lane);
+            if (!ball) {   // no hit: the last symbol of the leaf, or V-1 with [2^p-1, 2^p)
+                s = hit ? s0 + n - 1 : V - 1;
+                clo = base_run;
+                chi = hit ? base_run : (1u << prec);
+            }
+            if (lane == 0) {
+                kr_rc_state st = sh.dstate;
+                kr_bit_window wnd = sh.win;
+                kr_rc_consume(st.low, st.high, st.pending_or_value, clo, chi, prec, wnd);
+                st.bit_offset = wnd.pos;
+                D.states[row] = st;
+                D.out_syms[row] = s;
+                if (D.tokens) {
+                    const int cnt = D.tok_count ? D.tok_count[row] : 0;
+                    if (cnt >= 0 && cnt < D.tok_stride)
+                        D.tokens[(size_t)row * (size_t)D.tok_stride + cnt] = s;
+                    if (D.tok_count) D.tok_count[row] = cnt + 1;
+                }
             }
         }
     }

@@ -56,6 +56,28 @@ __device__ __forceinline__ kr_float4 add4(kr_float4 a, kr_float4 b) {
 // ---------------------------------------------------------------------------
 // Tile kernel (large M)
 // ---------------------------------------------------------------------------
+
+// Workgroup -> output tile. Workgroups are dealt to the 8 XCDs round robin
+// and each XCD has its own L2, so the launch holds 8 * ceil(T/8) workgroups
+// and XCD x takes the x-th contiguous eighth of the tile order; the order
+// walks groups of kGroupM row tiles, rows fastest, so an XCD reuses each
+// weight tile across the row tiles of a group and each A tile across the
+// column tiles of its band. Returns false for the padding workgroups.
+constexpr int kGroupM = 8;
+
+__device__ __forceinline__ bool tile_of(const kr_gemm_args& g, int BM, int BN, int& m_t, int& n_t) {
+    const int gy = (g.M + BM - 1) / BM, gx = (g.N + BN - 1) / BN;
+    const int T = gx * gy, per = (T + 7) / 8;
+    const int t = (int)(blockIdx.x & 7) * per + (int)(blockIdx.x >> 3);
+    if (t >= T) return false;
+    const int in_group = kGroupM * gx;
+    const int first_m = (t / in_group) * kGroupM;
+    const int gm = min(gy - first_m, kGroupM);
+    const int r = t % in_group;
+    m_t = first_m + r % gm;
+    n_t = r / gm;
+    return true;
+}
 template <int BM, int BN, int EP>
 __global__ void __launch_bounds__(256, 2) gemm_tile_kernel(kr_gemm_args g) {
     constexpr int WM = BM / 2, WN = BN / 2;
@@ -69,7 +91,9 @@ __global__ void __launch_bounds__(256, 2) gemm_tile_kernel(kr_gemm_args g) {
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave >> 1, wn = wave & 1;
-    const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+    int m_t, n_t;
+    if (!tile_of(g, BM, BN, m_t, n_t)) return;
+    const int m0 = m_t * BM, n0 = n_t * BN;
 
     kr_half8 ra[A_CHUNKS], rw[W_CHUNKS];
     auto load_tiles = [&](int k0) {
@@ -381,7 +405,8 @@ __global__ void __launch_bounds__(MAXT) gemm_panel_kernel(kr_gemm_multi mj) {
 
 template <int BM, int BN>
 int launch_tile(const kr_gemm_args& g, int ep, hipStream_t s) {
-    dim3 grid((g.N + BN - 1) / BN, (g.M + BM - 1) / BM);
+    const long long T = (long long)((g.N + BN - 1) / BN) * ((g.M + BM - 1) / BM);
+    const dim3 grid((unsigned)((T + 7) / 8 * 8));
     switch (ep) {
         case KR_EP_F32: gemm_tile_kernel<BM, BN, KR_EP_F32><<<grid, 256, 0, s>>>(g); break;
         case KR_EP_F16: gemm_tile_kernel<BM, BN, KR_EP_F16><<<grid, 256, 0, s>>>(g); break;

@@ -70,6 +70,46 @@ struct kr_bit_source {
     }
 };
 
+// The next 64 bits of a stream from bit `pos`, fetched with eight independent
+// byte loads (bytes at index >= limit read as zero). One decode step consumes
+// at most 26 bits (the narrowed interval is at least 2^6 wide and doubles per
+// bit), so a window taken before the step covers it; reads beyond the window
+// fall back to the byte reader.
+struct kr_bit_window {
+    const uint8_t* buf;
+    uint32_t limit;
+    uint32_t base;     // bit index of the window's first bit (multiple of 8)
+    uint32_t pos;
+    uint64_t w;
+    __device__ void open(const uint8_t* b, uint32_t lim, uint32_t bitpos) {
+        buf = b;
+        limit = lim;
+        pos = bitpos;
+        base = bitpos & ~7u;
+        const uint32_t byte = bitpos >> 3;
+        w = 0;
+        #pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const uint32_t bi = byte + (uint32_t)i;
+            const uint64_t v = bi < limit ? (uint64_t)buf[bi] : 0ull;
+            w |= v << (56 - 8 * i);
+        }
+    }
+    __device__ uint32_t get() {
+        const uint32_t off = pos - base;
+        uint32_t bit;
+        if (off < 64u) {
+            bit = (uint32_t)(w >> (63u - off)) & 1u;
+        } else {
+            const uint32_t byte = pos >> 3;
+            const uint32_t b = byte < limit ? (uint32_t)buf[byte] : 0u;
+            bit = (b >> (7u - (pos & 7u))) & 1u;
+        }
+        pos++;
+        return bit;
+    }
+};
+
 // Narrow [low, high] to the symbol's cumulative range [c_lo, c_hi) of 2^prec.
 __device__ __forceinline__ void kr_rc_narrow(uint32_t& low, uint32_t& high, uint32_t c_lo,
                                              uint32_t c_hi, int prec) {
@@ -121,9 +161,10 @@ __device__ __forceinline__ uint32_t kr_rc_target(uint32_t low, uint32_t high, ui
     return (uint32_t)(((off << prec) - 1ull) / span);
 }
 
+template <class Source>
 __device__ __forceinline__ void kr_rc_consume(uint32_t& low, uint32_t& high, uint32_t& value,
                                               uint32_t c_lo, uint32_t c_hi, int prec,
-                                              kr_bit_source& src) {
+                                              Source& src) {
     kr_rc_narrow(low, high, c_lo, c_hi, prec);
     for (;;) {
         uint32_t shift;
