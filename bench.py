@@ -185,7 +185,7 @@ def dominant_kernel_roofline(weights16, B):
     of one layer's matrix, every launch reads a different weight copy (64
     copies, 302 MB > the 256 MB Infinity Cache), so W comes from HBM.
     `traffic` is read from the committed counter summary
-    profiles/gemm_skinny_ffn_value_B256_traffic.json (rocprofv3 --pmc
+    profiles/gemm_panel_ffn_value_B256_traffic.json (rocprofv3 --pmc
     FETCH_SIZE / WRITE_SIZE, scaled by a 256 MiB copy calibration)."""
     import torch
     from krunch_amd import _lib, cpp_path
@@ -238,11 +238,11 @@ def dominant_kernel_roofline(weights16, B):
     alg_bytes = K * N * 2 + M * K * 2 + 3 * M * N * 2
     achieved = alg_bytes / avg_s / 1e9
     traffic = None
-    tfile = os.path.join(ROOT, "profiles", "gemm_skinny_ffn_value_B256_traffic.json")
+    tfile = os.path.join(ROOT, "profiles", "gemm_panel_ffn_value_B256_traffic.json")
     if os.path.exists(tfile) and M == 256:
         with open(tfile) as f:
             traffic = json.load(f).get("hbm_bytes_per_launch")
-    return {"kernel": "gemm_skinny_kernel<2,2> (stepped ffn value GEMM, M=%d K=%d N=%d, gated epilogue)"
+    return {"kernel": "gemm_panel_kernel<2,2,frag> (stepped ffn value GEMM, M=%d K=%d N=%d, gated epilogue)"
                       % (M, K, N),
             "bound": "hbm", "achieved": round(achieved, 2), "peak": MI355X_HBM_PEAK / 1e9,
             "unit": "GB/s", "frac": round(achieved / (MI355X_HBM_PEAK / 1e9), 4), "traffic": traffic,
