@@ -169,6 +169,24 @@ int kr_det_matmul_packed(const uint16_t* xf, int M, int K, const uint16_t* Wf, i
                          long long ldo, int epilogue, const uint16_t* res, const uint16_t* gate,
                          int out_packed, void* stream);
 
+/* w8a8 (the reference only sketches an int8 path,
+ * docs/INT8_WEIGHTS_DESIGN.md): symmetric int8 with one fp32 scale per row,
+ * s = max|x| / 127 (1 when the row is zero), q = clamp(rint(x / s), -127, 127).
+ * Rows are tokens for activations and output channels (rows of Wt) for
+ * weights. q is [M, K] row-major, or fragment-packed (packed = 1, rows padded
+ * to 16, kr_quant_bytes) for the small-M GEMM; K % 64 == 0. */
+size_t kr_quant_bytes(int M, int K, int packed);
+int kr_quantize_rows(const uint16_t* x, long long ldx, int M, int K, int8_t* q, float* scales,
+                     int packed, void* stream);
+
+/* int8 GEMM: acc = sum_k xq[m,k] * wq[n,k] exactly in int32, value =
+ * (float(acc) * sa[m]) * sw[n], then the epilogue of kr_det_matmul. packed = 1:
+ * xq and wq fragment-packed (wq packed by kr_pack_fragments on its 16-bit
+ * view, K/2 columns), M <= 512; packed = 0: both row-major [*, K]. */
+int kr_det_matmul_i8(const int8_t* xq, const float* sa, int M, int K, const int8_t* wq,
+                     const float* sw, int N, void* out, long long ldo, int epilogue,
+                     const uint16_t* res, const uint16_t* gate, int packed, void* stream);
+
 typedef struct kr_layer_weights {
     const void *ln1_w, *ln1_b;            /* fp16 [C] */
     const void *tm_k, *tm_v, *tm_r;       /* fp16 [C] */

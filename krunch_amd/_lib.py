@@ -55,6 +55,9 @@ _SIGS = {
     "kr_fragment_bytes": ([I, I], ctypes.c_size_t),
     "kr_pack_fragments": ([P, LL, I, I, P, P], I),
     "kr_det_matmul_packed": ([P, I, I, P, I, P, LL, I, P, P, I, P], I),
+    "kr_quant_bytes": ([I, I, I], ctypes.c_size_t),
+    "kr_quantize_rows": ([P, LL, I, I, P, P, I, P], I),
+    "kr_det_matmul_i8": ([P, P, I, I, P, P, I, P, LL, I, P, P, I, P], I),
     "kr_prepare_decay": ([P, P, I, P], I),
     "kr_state_bytes": ([I, I, I], SZ),
     "kr_state_init": ([P, I, I, I, P], I),

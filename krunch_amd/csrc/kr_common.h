@@ -14,6 +14,7 @@ typedef _Float16 kr_half;
 typedef _Float16 kr_half4 __attribute__((ext_vector_type(4)));
 typedef _Float16 kr_half8 __attribute__((ext_vector_type(8)));
 typedef float kr_float4 __attribute__((ext_vector_type(4)));
+typedef int kr_int4 __attribute__((ext_vector_type(4)));
 
 // ---------------------------------------------------------------------------
 // Range-coder constants (32-bit state; the coding spec is a 32-bit range coder

@@ -25,6 +25,11 @@ struct kr_gemm_args {
     const kr_half* Wf;  // W^T fragment-packed (kr_frag_index), or null; small-M path only
     int a_frag;         // A is fragment-packed (small-M path only; needs Wf)
     int out_frag;       // fp16 output written fragment-packed as a K = N operand
+    // w8a8: A and W^T hold int8 (pointers reinterpreted; lda/ldw in bytes),
+    // acc = exact int32 sum, value = (float(acc) * sa[m]) * sw[n], then the epilogue.
+    int i8;
+    const float* sa;    // [M] per-row (per-token) activation scales
+    const float* sw;    // [N] per-output-channel weight scales
 };
 
 // Fragment-packed layout of an [R, K] fp16 operand (K % 32 == 0, R padded to
@@ -36,6 +41,12 @@ struct kr_gemm_args {
 __host__ __device__ inline size_t kr_frag_index(long long r, long long k, long long K) {
     return ((size_t)((r >> 4) * (K >> 5) + (k >> 5)) * 64 +
             (size_t)((r & 15) + 16 * ((k & 31) >> 3))) * 8 + (size_t)(k & 7);
+}
+// int8 operands use the same bytes per block: a 16 x 64 int8 block is the
+// 16 x 32 block of the 16-bit view (byte pairs), so lane r%16 + 16*((k%64)/16)
+// holds the 16 consecutive k of one row - the v_mfma_i32_16x16x64_i8 operand.
+__host__ __device__ inline size_t kr_frag_index_i8(long long r, long long k, long long K) {
+    return 2 * kr_frag_index(r, k >> 1, K >> 1) + (size_t)(k & 1);
 }
 // Rows of a fragment-packed operand with R logical rows (multiple of 16).
 __host__ __device__ inline long long kr_frag_rows(long long R) { return (R + 15) / 16 * 16; }
@@ -57,11 +68,12 @@ struct kr_gemm_multi {
 };
 
 // Launch C = A @ W (W given transposed), kernel and tile shape chosen from M.
-// Reduction contract, whatever the kernel: for every output element,
+// Reduction contract (fp16), whatever the kernel: for every output element,
 //   P_s = chain of v_mfma_f32_16x16x32_f16 over k = 256s, 256s+32, ..., 256s+224
 //         starting from zero (s = 0 .. K/256 - 1),
 //   acc = P_0; acc = acc + P_1; ...; acc = acc + P_{S-1}   (fp32 adds, in order),
-// then the epilogue. A row therefore gets identical bits for any M.
+// then the epilogue. A row therefore gets identical bits for any M. The int8
+// path accumulates exactly in int32, so any order gives the same bits.
 int kr_gemm_launch(const kr_gemm_args& g, int epilogue, hipStream_t stream);
 // Several products; on the small-M path those sharing M and K run in one
 // launch (independent outputs), otherwise they are launched in order.

@@ -19,6 +19,7 @@
 //    added in slice order through LDS and the epilogue is shared out over the
 //    waves. Parallelism comes from the K slices, not from M.
 #include <algorithm>
+#include <type_traits>
 
 #include "kr_gemm.h"
 
@@ -78,7 +79,11 @@ __device__ __forceinline__ bool tile_of(const kr_gemm_args& g, int BM, int BN, i
     n_t = r / gm;
     return true;
 }
-template <int BM, int BN, int EP>
+__device__ __forceinline__ kr_int4 as_i4(kr_half8 v) { return __builtin_bit_cast(kr_int4, v); }
+
+// I8: int8 operands moved as 16-bit pairs (a 64-half K tile = 128 int8 k; a
+// 32-half k step = one v_mfma_i32_16x16x64_i8), int32 accumulation.
+template <int BM, int BN, int EP, bool I8>
 __global__ void __launch_bounds__(256, 2) gemm_tile_kernel(kr_gemm_args g) {
     constexpr int WM = BM / 2, WN = BN / 2;
     constexpr int TM = WM / 16, TN = WN / 16;
@@ -94,6 +99,8 @@ __global__ void __launch_bounds__(256, 2) gemm_tile_kernel(kr_gemm_args g) {
     int m_t, n_t;
     if (!tile_of(g, BM, BN, m_t, n_t)) return;
     const int m0 = m_t * BM, n0 = n_t * BN;
+    const int K16 = I8 ? g.K >> 1 : g.K;
+    const long long lda16 = I8 ? g.lda >> 1 : g.lda, ldw16 = I8 ? g.ldw >> 1 : g.ldw;
 
     kr_half8 ra[A_CHUNKS], rw[W_CHUNKS];
     auto load_tiles = [&](int k0) {
@@ -102,7 +109,7 @@ __global__ void __launch_bounds__(256, 2) gemm_tile_kernel(kr_gemm_args g) {
             const int c = tid + 256 * i, r = c >> 3, col = (c & 7) * 8;
             const int m = m0 + r;
             if (m < g.M)
-                ra[i] = *reinterpret_cast<const kr_half8*>(g.A + (size_t)m * g.lda + k0 + col);
+                ra[i] = *reinterpret_cast<const kr_half8*>(g.A + (size_t)m * lda16 + k0 + col);
             else
                 ra[i] = kr_half8{0, 0, 0, 0, 0, 0, 0, 0};
         }
@@ -111,7 +118,7 @@ __global__ void __launch_bounds__(256, 2) gemm_tile_kernel(kr_gemm_args g) {
             const int c = tid + 256 * i, r = c >> 3, col = (c & 7) * 8;
             const int n = n0 + r;
             if (n < g.N)
-                rw[i] = *reinterpret_cast<const kr_half8*>(g.Wt + (size_t)n * g.ldw + k0 + col);
+                rw[i] = *reinterpret_cast<const kr_half8*>(g.Wt + (size_t)n * ldw16 + k0 + col);
             else
                 rw[i] = kr_half8{0, 0, 0, 0, 0, 0, 0, 0};
         }
@@ -129,16 +136,18 @@ __global__ void __launch_bounds__(256, 2) gemm_tile_kernel(kr_gemm_args g) {
         }
     };
 
-    kr_float4 acc[TM][TN], tot[TM][TN];
+    typedef typename std::conditional<I8, kr_int4, kr_float4>::type Acc;
+    Acc acc[TM][TN];
+    kr_float4 tot[TM][TN];
     #pragma unroll
     for (int i = 0; i < TM; i++)
         #pragma unroll
         for (int j = 0; j < TN; j++) {
-            acc[i][j] = kr_float4{0.f, 0.f, 0.f, 0.f};
-            tot[i][j] = acc[i][j];
+            acc[i][j] = Acc{0, 0, 0, 0};
+            tot[i][j] = kr_float4{0.f, 0.f, 0.f, 0.f};
         }
 
-    const int KT = g.K / kBK;
+    const int KT = K16 / kBK;
     constexpr int TILES_PER_SPLIT = kKS / kBK;
     load_tiles(0);
     const int lrow = lane & 15, lk = (lane >> 4) * 8;
@@ -161,17 +170,25 @@ __global__ void __launch_bounds__(256, 2) gemm_tile_kernel(kr_gemm_args g) {
             #pragma unroll
             for (int i = 0; i < TM; i++)
                 #pragma unroll
-                for (int j = 0; j < TN; j++)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[i], b[j], acc[i][j], 0, 0, 0);
+                for (int j = 0; j < TN; j++) {
+                    if constexpr (I8)
+                        acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(as_i4(a[i]), as_i4(b[j]),
+                                                                         acc[i][j], 0, 0, 0);
+                    else
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[i], b[j], acc[i][j],
+                                                                          0, 0, 0);
+                }
         }
-        if ((kt + 1) % TILES_PER_SPLIT == 0) {     // end of a 256-wide K slice
+        if (!I8 && (kt + 1) % TILES_PER_SPLIT == 0) {     // end of a 256-wide K slice
             const bool first = kt + 1 == TILES_PER_SPLIT;
             #pragma unroll
             for (int i = 0; i < TM; i++)
                 #pragma unroll
                 for (int j = 0; j < TN; j++) {
-                    tot[i][j] = first ? acc[i][j] : add4(tot[i][j], acc[i][j]);
-                    acc[i][j] = kr_float4{0.f, 0.f, 0.f, 0.f};
+                    if constexpr (!I8) {
+                        tot[i][j] = first ? acc[i][j] : add4(tot[i][j], acc[i][j]);
+                        acc[i][j] = Acc{0, 0, 0, 0};
+                    }
                 }
         }
     }
@@ -185,7 +202,12 @@ __global__ void __launch_bounds__(256, 2) gemm_tile_kernel(kr_gemm_args g) {
             for (int r = 0; r < 4; r++) {
                 const int m = m0 + wm * WM + i * 16 + (lane >> 4) * 4 + r;
                 const int n = n0 + wn * WN + j * 16 + (lane & 15);
-                if (m < g.M && n < g.N) store_one<EP>(g, m, n, tot[i][j][r]);
+                if (m < g.M && n < g.N) {
+                    float v;
+                    if constexpr (I8) v = __fmul_rn(__fmul_rn((float)acc[i][j][r], g.sa[m]), g.sw[n]);
+                    else v = tot[i][j][r];
+                    store_one<EP>(g, m, n, v);
+                }
             }
 }
 
@@ -221,9 +243,13 @@ __global__ void __launch_bounds__(256, 2) gemm_tile_kernel(kr_gemm_args g) {
 // weight byte is fetched into one L2.
 constexpr int kEpiPrefetch = 4;   // epilogue tiles per wave with prefetched res/gate
 
-template <int TM, int NS, bool FRAG, int MAXT>
+template <int TM, int NS, bool FRAG, int MAXT, bool I8>
 __global__ void __launch_bounds__(MAXT) gemm_panel_kernel(kr_gemm_multi mj) {
     constexpr int TT = TM * NS;
+    // 1 KB operand blocks per wave slice: 8 x (16x32 fp16) or 4 x (16x64 int8);
+    // either way a wave covers 256 k. int8 operands move as 16-bit pairs.
+    constexpr int QPS = I8 ? 4 : 8;
+    typedef typename std::conditional<I8, kr_int4, kr_float4>::type Acc;
     extern __shared__ __attribute__((aligned(16))) float part_lds[];   // [S][TT][256]
     const int lane = threadIdx.x & 63, s = threadIdx.x >> 6;
     // Job of this workgroup; fields are copied with constant indices so every
@@ -250,37 +276,38 @@ __global__ void __launch_bounds__(MAXT) gemm_panel_kernel(kr_gemm_multi mj) {
     }
     const int m0 = m_t * 16 * TM, n0 = n_g * 16 * NS;
     const int last_mb = (g.M - 1) >> 4, last_nb = (g.N - 1) >> 4;
+    const long long lda16 = I8 ? g.lda >> 1 : g.lda, ldw16 = I8 ? g.ldw >> 1 : g.ldw;
 
     // ---- operand loads: A once, W panels double buffered
-    kr_half8 a[TM][8];
-    kr_half8 b[2][8];
-    const int kb = g.K >> 5;
-    auto load_w = [&](int t, kr_half8 (&dst)[8]) {
+    kr_half8 a[TM][QPS];
+    kr_half8 b[2][QPS];
+    const int kb = (I8 ? g.K >> 1 : g.K) >> 5;   // 1 KB blocks per row
+    auto load_w = [&](int t, kr_half8 (&dst)[QPS]) {
         // panels beyond N re-read the last one; their outputs are never stored
         if constexpr (FRAG) {
             const int nb = min((n0 >> 4) + t, last_nb);
-            const kr_half* bp = g.Wf + ((size_t)nb * kb + 8 * s) * 512 + lane * 8;
+            const kr_half* bp = g.Wf + ((size_t)nb * kb + QPS * s) * 512 + lane * 8;
             #pragma unroll
-            for (int q = 0; q < 8; q++) dst[q] = *reinterpret_cast<const kr_half8*>(bp + 512 * q);
+            for (int q = 0; q < QPS; q++) dst[q] = *reinterpret_cast<const kr_half8*>(bp + 512 * q);
         } else {
             const int r = min(n0 + 16 * t + (lane & 15), g.N - 1);
-            const kr_half* bp = g.Wt + (size_t)r * g.ldw + s * kKS + (lane >> 4) * 8;
+            const kr_half* bp = g.Wt + (size_t)r * ldw16 + s * QPS * 32 + (lane >> 4) * 8;
             #pragma unroll
-            for (int q = 0; q < 8; q++) dst[q] = *reinterpret_cast<const kr_half8*>(bp + 32 * q);
+            for (int q = 0; q < QPS; q++) dst[q] = *reinterpret_cast<const kr_half8*>(bp + 32 * q);
         }
     };
     #pragma unroll
     for (int i = 0; i < TM; i++) {
         if constexpr (FRAG) {
             const int mb = min((m0 >> 4) + i, last_mb);
-            const kr_half* ap = g.A + ((size_t)mb * kb + 8 * s) * 512 + lane * 8;
+            const kr_half* ap = g.A + ((size_t)mb * kb + QPS * s) * 512 + lane * 8;
             #pragma unroll
-            for (int q = 0; q < 8; q++) a[i][q] = *reinterpret_cast<const kr_half8*>(ap + 512 * q);
+            for (int q = 0; q < QPS; q++) a[i][q] = *reinterpret_cast<const kr_half8*>(ap + 512 * q);
         } else {
             const int r = min(m0 + 16 * i + (lane & 15), g.M - 1);
-            const kr_half* ap = g.A + (size_t)r * g.lda + s * kKS + (lane >> 4) * 8;
+            const kr_half* ap = g.A + (size_t)r * lda16 + s * QPS * 32 + (lane >> 4) * 8;
             #pragma unroll
-            for (int q = 0; q < 8; q++) a[i][q] = *reinterpret_cast<const kr_half8*>(ap + 32 * q);
+            for (int q = 0; q < QPS; q++) a[i][q] = *reinterpret_cast<const kr_half8*>(ap + 32 * q);
         }
     }
     load_w(0, b[0]);
@@ -318,18 +345,34 @@ __global__ void __launch_bounds__(MAXT) gemm_panel_kernel(kr_gemm_multi mj) {
     __builtin_amdgcn_sched_barrier(0);     // loads in flight before the MFMAs
 
     // ---- MFMA chains, one per (row block, panel)
-    kr_float4 p[TM][NS];
+    Acc p[TM][NS];
     #pragma unroll
     for (int t = 0; t < NS; t++) {
         #pragma unroll
         for (int i = 0; i < TM; i++) {
-            p[i][t] = kr_float4{0.f, 0.f, 0.f, 0.f};
+            p[i][t] = Acc{0, 0, 0, 0};
             #pragma unroll
-            for (int q = 0; q < 8; q++)
-                p[i][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(b[t & 1][q], a[i][q], p[i][t], 0, 0, 0);
+            for (int q = 0; q < QPS; q++) {
+                if constexpr (I8)
+                    p[i][t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(as_i4(b[t & 1][q]),
+                                                                   as_i4(a[i][q]), p[i][t], 0, 0, 0);
+                else
+                    p[i][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(b[t & 1][q], a[i][q], p[i][t],
+                                                                    0, 0, 0);
+            }
         }
         if (t + 2 < NS) load_w(t + 2, b[t & 1]);
     }
+    // int8: exact int32 sums dequantised once per output
+    auto dequant = [&](int t, kr_int4 acc) -> kr_float4 {
+        int m, nb;
+        tile_mn(t, m, nb);
+        const float sa = g.sa[min(m, g.M - 1)];
+        kr_float4 y;
+        #pragma unroll
+        for (int r = 0; r < 4; r++) y[r] = __fmul_rn(__fmul_rn((float)acc[r], sa), g.sw[min(nb + r, g.N - 1)]);
+        return y;
+    };
 
     // ---- slice partials in LDS, then each tile summed in slice order
     auto epilogue = [&](int t, int e, kr_float4 acc) {
@@ -385,35 +428,37 @@ __global__ void __launch_bounds__(MAXT) gemm_panel_kernel(kr_gemm_multi mj) {
     };
     if (S == 1) {
         #pragma unroll
-        for (int t = 0; t < TT; t++) epilogue(t, t, p[t / NS][t % NS]);
+        for (int t = 0; t < TT; t++) {
+            if constexpr (I8) epilogue(t, t, dequant(t, p[t / NS][t % NS]));
+            else epilogue(t, t, p[t / NS][t % NS]);
+        }
         return;
     }
     #pragma unroll
     for (int t = 0; t < TT; t++)
-        *reinterpret_cast<kr_float4*>(part_lds + ((size_t)s * TT + t) * 256 + lane * 4) =
-            p[t / NS][t % NS];
+        *reinterpret_cast<Acc*>(part_lds + ((size_t)s * TT + t) * 256 + lane * 4) = p[t / NS][t % NS];
     __syncthreads();
     for (int e = 0; e < my_tiles; e++) {
         const int t = s + e * S;
-        kr_float4 acc = *reinterpret_cast<const kr_float4*>(part_lds + (size_t)t * 256 + lane * 4);
+        Acc acc = *reinterpret_cast<const Acc*>(part_lds + (size_t)t * 256 + lane * 4);
         for (int q = 1; q < S; q++)
-            acc = add4(acc, *reinterpret_cast<const kr_float4*>(
-                                part_lds + ((size_t)q * TT + t) * 256 + lane * 4));
-        epilogue(t, e, acc);
+            acc = acc + *reinterpret_cast<const Acc*>(part_lds + ((size_t)q * TT + t) * 256 + lane * 4);
+        if constexpr (I8) epilogue(t, e, dequant(t, acc));
+        else epilogue(t, e, acc);
     }
 }
 
-template <int BM, int BN>
+template <int BM, int BN, bool I8>
 int launch_tile(const kr_gemm_args& g, int ep, hipStream_t s) {
     const long long T = (long long)((g.N + BN - 1) / BN) * ((g.M + BM - 1) / BM);
     const dim3 grid((unsigned)((T + 7) / 8 * 8));
     switch (ep) {
-        case KR_EP_F32: gemm_tile_kernel<BM, BN, KR_EP_F32><<<grid, 256, 0, s>>>(g); break;
-        case KR_EP_F16: gemm_tile_kernel<BM, BN, KR_EP_F16><<<grid, 256, 0, s>>>(g); break;
-        case KR_EP_SIGMOID: gemm_tile_kernel<BM, BN, KR_EP_SIGMOID><<<grid, 256, 0, s>>>(g); break;
-        case KR_EP_RELUSQ: gemm_tile_kernel<BM, BN, KR_EP_RELUSQ><<<grid, 256, 0, s>>>(g); break;
-        case KR_EP_RESID: gemm_tile_kernel<BM, BN, KR_EP_RESID><<<grid, 256, 0, s>>>(g); break;
-        case KR_EP_GATED: gemm_tile_kernel<BM, BN, KR_EP_GATED><<<grid, 256, 0, s>>>(g); break;
+        case KR_EP_F32: gemm_tile_kernel<BM, BN, KR_EP_F32, I8><<<grid, 256, 0, s>>>(g); break;
+        case KR_EP_F16: gemm_tile_kernel<BM, BN, KR_EP_F16, I8><<<grid, 256, 0, s>>>(g); break;
+        case KR_EP_SIGMOID: gemm_tile_kernel<BM, BN, KR_EP_SIGMOID, I8><<<grid, 256, 0, s>>>(g); break;
+        case KR_EP_RELUSQ: gemm_tile_kernel<BM, BN, KR_EP_RELUSQ, I8><<<grid, 256, 0, s>>>(g); break;
+        case KR_EP_RESID: gemm_tile_kernel<BM, BN, KR_EP_RESID, I8><<<grid, 256, 0, s>>>(g); break;
+        case KR_EP_GATED: gemm_tile_kernel<BM, BN, KR_EP_GATED, I8><<<grid, 256, 0, s>>>(g); break;
         default: return kr_fail(KR_EINVAL, "unknown epilogue %d", ep);
     }
     KR_LAUNCHED();
@@ -424,7 +469,7 @@ struct PanelShape {
     int TM, NS;
 };
 
-template <int TM, int NS, bool FRAG, int MAXT>
+template <int TM, int NS, bool FRAG, int MAXT, bool I8>
 int launch_panel(kr_gemm_multi mj, hipStream_t s) {
     const int S = mj.job[0].K / kKS;
     int total = 0;
@@ -434,7 +479,7 @@ int launch_panel(kr_gemm_multi mj, hipStream_t s) {
         total += mj.tiles[j];
     }
     const size_t lds = S > 1 ? (size_t)S * TM * NS * 256 * sizeof(float) : 0;
-    gemm_panel_kernel<TM, NS, FRAG, MAXT><<<total, dim3(64 * S), lds, s>>>(mj);
+    gemm_panel_kernel<TM, NS, FRAG, MAXT, I8><<<total, dim3(64 * S), lds, s>>>(mj);
     KR_LAUNCHED();
     return KR_OK;
 }
@@ -462,7 +507,7 @@ long long panel_cost(const kr_gemm_multi& mj, PanelShape sh) {
     return ((wgs + 255) / 256) * per_wg * 4096 - std::min<long long>(wgs, 256);
 }
 
-template <bool FRAG, int MAXT, size_t N>
+template <bool FRAG, int MAXT, bool I8, size_t N>
 int launch_best(const kr_gemm_multi& mj, const PanelShape (&shapes)[N], hipStream_t s) {
     PanelShape best = shapes[0];
     long long best_cost = panel_cost(mj, best);
@@ -471,7 +516,7 @@ int launch_best(const kr_gemm_multi& mj, const PanelShape (&shapes)[N], hipStrea
         if (c < best_cost) { best_cost = c; best = shapes[i]; }
     }
 #define KR_PANEL(TM_, NS_) \
-    if (best.TM == TM_ && best.NS == NS_) return launch_panel<TM_, NS_, FRAG, MAXT>(mj, s);
+    if (best.TM == TM_ && best.NS == NS_) return launch_panel<TM_, NS_, FRAG, MAXT, I8>(mj, s);
     if constexpr (MAXT == 256 || MAXT == 768) {
         KR_PANEL(1, 1) KR_PANEL(1, 2) KR_PANEL(2, 1) KR_PANEL(2, 2)
     } else {
@@ -481,12 +526,12 @@ int launch_best(const kr_gemm_multi& mj, const PanelShape (&shapes)[N], hipStrea
     return kr_fail(KR_EINVAL, "gemm: no panel shape");
 }
 
-template <bool FRAG>
+template <bool FRAG, bool I8>
 int launch_small(const kr_gemm_multi& mj, hipStream_t s) {
     const int S = mj.job[0].K / kKS;
-    if (S <= 4) return launch_best<FRAG, 256>(mj, kShapes256, s);
-    if (S <= 12) return launch_best<FRAG, 768>(mj, kShapes768, s);
-    return launch_best<FRAG, 1024>(mj, kShapes1024, s);
+    if (S <= 4) return launch_best<FRAG, 256, I8>(mj, kShapes256, s);
+    if (S <= 12) return launch_best<FRAG, 768, I8>(mj, kShapes768, s);
+    return launch_best<FRAG, 1024, I8>(mj, kShapes1024, s);
 }
 
 // Pack Wt [N, K] (row stride ld) into the fragment layout; rows N..N16-1 are zero.
@@ -539,6 +584,9 @@ int check_args(const kr_gemm_args& g, int ep) {
                                ep != KR_EP_GATED && ((uintptr_t)g.out & 7) == 0),
                "gemm: fragment-packed output needs N %% 32 == 0 and an elementwise fp16 epilogue");
     KR_REQUIRE(ep >= KR_EP_F32 && ep <= KR_EP_GATED, "gemm: unknown epilogue %d", ep);
+    KR_REQUIRE(!g.i8 || (g.sa && g.sw && (g.a_frag || g.lda % 16 == 0) &&
+                         (!g.Wt || g.ldw % 16 == 0)),
+               "gemm: int8 needs scales and 16-byte aligned rows (lda/ldw multiples of 16)");
     KR_REQUIRE((ep != KR_EP_RESID && ep != KR_EP_GATED) || g.res, "gemm: residual missing");
     KR_REQUIRE(ep != KR_EP_GATED || g.gate, "gemm: gate missing");
     return KR_OK;
@@ -552,8 +600,10 @@ int kr_gemm_launch_multi(const kr_gemm_args* jobs, const int* eps, int njobs, hi
     }
     const int M = jobs[0].M, K = jobs[0].K;
     bool same = true, small_n = true, frag = jobs[0].a_frag != 0, any_frag = false;
+    const bool i8 = jobs[0].i8 != 0;
     for (int j = 1; j < njobs; j++)
-        same = same && jobs[j].M == M && jobs[j].K == K && (jobs[j].a_frag != 0) == frag;
+        same = same && jobs[j].M == M && jobs[j].K == K && (jobs[j].a_frag != 0) == frag &&
+               (jobs[j].i8 != 0) == i8;
     for (int j = 0; j < njobs; j++) {
         small_n = small_n && jobs[j].N < KR_GEMM_SMALL_MAX_N;
         any_frag = any_frag || jobs[j].a_frag || jobs[j].out_frag;
@@ -567,18 +617,25 @@ int kr_gemm_launch_multi(const kr_gemm_args* jobs, const int* eps, int njobs, hi
         kr_gemm_multi mj{};
         mj.njobs = njobs;
         for (int j = 0; j < njobs; j++) { mj.job[j] = jobs[j]; mj.ep[j] = eps[j]; }
-        if (frag) return launch_small<true>(mj, s);
+        if (frag) return i8 ? launch_small<true, true>(mj, s) : launch_small<true, false>(mj, s);
         // row-major A: fragment weights are not used, the row-major copy must exist
         for (int j = 0; j < njobs; j++) KR_REQUIRE(jobs[j].Wt, "gemm: row-major W missing");
-        return launch_small<false>(mj, s);
+        return i8 ? launch_small<false, true>(mj, s) : launch_small<false, false>(mj, s);
     }
     for (int j = 0; j < njobs; j++) {
         const kr_gemm_args& g = jobs[j];
         KR_REQUIRE(g.Wt, "gemm: row-major W missing");
         int rc;
-        if (g.M >= 4096) rc = launch_tile<128, 128>(g, eps[j], s);
-        else if (g.M > KR_GEMM_SMALL_M) rc = launch_tile<64, 64>(g, eps[j], s);
-        else rc = launch_tile<64, 128>(g, eps[j], s);   // small M, huge N (the head)
+        if (g.i8) {
+            if (g.M >= 4096) rc = launch_tile<128, 128, true>(g, eps[j], s);
+            else rc = launch_tile<64, 64, true>(g, eps[j], s);
+        } else if (g.M >= 4096) {
+            rc = launch_tile<128, 128, false>(g, eps[j], s);
+        } else if (g.M > KR_GEMM_SMALL_M) {
+            rc = launch_tile<64, 64, false>(g, eps[j], s);
+        } else {
+            rc = launch_tile<64, 128, false>(g, eps[j], s);   // small M, huge N (the head)
+        }
         if (rc) return rc;
     }
     return KR_OK;

@@ -1,0 +1,105 @@
+// w8a8 quantisation: symmetric int8 with fp32 scales,
+// one scale per row. Used for the weights (rows of W^T = output channels) at
+// preparation time and for activations (rows = tokens) on the fly.
+//
+//   amax = max_k |x[k]|;  s = amax / 127 (s = 1 when amax = 0)
+//   q[k] = clamp(rint(x[k] / s), -127, 127)          (IEEE divide, ties to even)
+//
+// so the int8 GEMM value (float(sum q_a q_w) * s_a) * s_w approximates x @ W.
+// The output is row-major [M, K] int8 or fragment-packed (kr_frag_index_i8),
+// the operand layout of the small-M int8 GEMM.
+#include "kr_gemm.h"
+
+namespace {
+
+__device__ __forceinline__ float wave_maxf(float v) {
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+    return v;
+}
+
+__device__ __forceinline__ uint32_t pack4(const float (&x)[4], float s) {
+    uint32_t w = 0;
+    #pragma unroll
+    for (int r = 0; r < 4; r++) {
+        float q = rintf(x[r] / s);
+        q = fminf(fmaxf(q, -127.0f), 127.0f);
+        w |= ((uint32_t)(uint8_t)(int8_t)(int)q) << (8 * r);
+    }
+    return w;
+}
+
+// One wave per row; lane l owns the 4-column groups at 256*i + 4*l.
+__global__ void __launch_bounds__(256) row_quant_kernel(const kr_half* __restrict__ x, long long ldx,
+                                                        int M, int K, int8_t* __restrict__ q,
+                                                        float* __restrict__ scales, int packed) {
+    const int lane = threadIdx.x & 63;
+    const int row = (blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+    if (row >= M) return;
+    const kr_half* xr = x + (size_t)row * (size_t)ldx;
+    float amax = 0.0f;
+    for (int c = 4 * lane; c < K; c += 256) {
+        const kr_half4 h = *reinterpret_cast<const kr_half4*>(xr + c);
+        #pragma unroll
+        for (int r = 0; r < 4; r++) amax = fmaxf(amax, fabsf((float)h[r]));
+    }
+    amax = wave_maxf(amax);
+    const float s = amax > 0.0f ? amax / 127.0f : 1.0f;
+    for (int c = 4 * lane; c < K; c += 256) {
+        const kr_half4 h = *reinterpret_cast<const kr_half4*>(xr + c);
+        const float v[4] = {(float)h[0], (float)h[1], (float)h[2], (float)h[3]};
+        const size_t o = packed ? kr_frag_index_i8(row, c, K) : (size_t)row * (size_t)K + c;
+        *reinterpret_cast<uint32_t*>(q + o) = pack4(v, s);
+    }
+    if (lane == 0) scales[row] = s;
+}
+
+}  // namespace
+
+int kr_impl_quantize_rows(const void* x, long long ldx, int M, int K, void* q, float* scales,
+                          int packed, hipStream_t s) {
+    KR_REQUIRE(x && q && scales && M >= 0 && K >= 64 && K % 64 == 0 && ldx >= K && ldx % 4 == 0,
+               "quantize: bad args (K must be a multiple of 64)");
+    KR_REQUIRE(((uintptr_t)x & 7) == 0 && ((uintptr_t)q & 3) == 0, "quantize: misaligned pointer");
+    if (M == 0) return KR_OK;
+    row_quant_kernel<<<(M + 3) / 4, 256, 0, s>>>(reinterpret_cast<const kr_half*>(x), ldx, M, K,
+                                                 reinterpret_cast<int8_t*>(q), scales, packed);
+    KR_LAUNCHED();
+    return KR_OK;
+}
+
+extern "C" {
+
+size_t kr_quant_bytes(int M, int K, int packed) {
+    if (M < 0 || K < 64 || K % 64) return 0;
+    return (size_t)(packed ? kr_frag_rows(M) : M) * (size_t)K;
+}
+
+int kr_quantize_rows(const uint16_t* x, long long ldx, int M, int K, int8_t* q, float* scales,
+                     int packed, void* stream) {
+    return kr_impl_quantize_rows(x, ldx, M, K, q, scales, packed, kr_stream(stream));
+}
+
+int kr_det_matmul_i8(const int8_t* xq, const float* sa, int M, int K, const int8_t* wq,
+                     const float* sw, int N, void* out, long long ldo, int epilogue,
+                     const uint16_t* res, const uint16_t* gate, int packed, void* stream) {
+    kr_gemm_args g{};
+    g.A = reinterpret_cast<const kr_half*>(xq);
+    g.lda = K;
+    if (packed) g.Wf = reinterpret_cast<const kr_half*>(wq);
+    else g.Wt = reinterpret_cast<const kr_half*>(wq);
+    g.ldw = K;
+    g.out = out;
+    g.ldo = ldo;
+    g.res = reinterpret_cast<const kr_half*>(res);
+    g.gate = reinterpret_cast<const kr_half*>(gate);
+    g.M = M;
+    g.N = N;
+    g.K = K;
+    g.a_frag = packed ? 1 : 0;
+    g.i8 = 1;
+    g.sa = sa;
+    g.sw = sw;
+    return kr_gemm_launch(g, epilogue, kr_stream(stream));
+}
+
+}  // extern "C"
