@@ -187,6 +187,17 @@ int kr_det_matmul_i8(const int8_t* xq, const float* sa, int M, int K, const int8
                      const float* sw, int N, void* out, long long ldo, int epilogue,
                      const uint16_t* res, const uint16_t* gate, int packed, void* stream);
 
+/* w8a8 copy of one matrix (kr_quantize_rows on Wt: one scale per output channel). */
+typedef struct kr_matrix_q8 {
+    const int8_t* q;                      /* [N, K] row-major int8 (rows = output channels) */
+    const int8_t* qf;                     /* the same fragment-packed (16-bit view, K/2 columns) */
+    const float* scale;                   /* [N] */
+} kr_matrix_q8;
+
+typedef struct kr_layer_q8 {
+    kr_matrix_q8 K, V, R, O, fK, fV, fR;
+} kr_layer_q8;
+
 typedef struct kr_layer_weights {
     const void *ln1_w, *ln1_b;            /* fp16 [C] */
     const void *tm_k, *tm_v, *tm_r;       /* fp16 [C] */
@@ -201,6 +212,10 @@ typedef struct kr_layer_weights {
     /* Fragment-packed copies of the seven matrices above (kr_pack_fragments),
      * read by the small-M (B*T <= 512) path; all NULL = use the row-major ones. */
     const void *Kf, *Vf, *Rf, *Of, *fKf, *fVf, *fRf;
+    /* w8a8 codec: int8 copies of the seven matrices; the
+     * layer then runs its GEMMs on int8 MFMA with per-token activation
+     * quantisation. NULL = fp16 codec. The head stays fp16 either way. */
+    const kr_layer_q8* q8;
 } kr_layer_weights;
 
 typedef struct kr_model_weights {

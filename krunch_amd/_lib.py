@@ -18,11 +18,19 @@ U32 = ctypes.c_uint32
 SZ = ctypes.c_size_t
 
 
+class KrMatrixQ8(ctypes.Structure):
+    _fields_ = [("q", P), ("qf", P), ("scale", P)]
+
+
+class KrLayerQ8(ctypes.Structure):
+    _fields_ = [(n, KrMatrixQ8) for n in ("K", "V", "R", "O", "fK", "fV", "fR")]
+
+
 class KrLayerWeights(ctypes.Structure):
     _fields_ = [(n, P) for n in (
         "ln1_w", "ln1_b", "tm_k", "tm_v", "tm_r", "decay", "first",
         "Kt", "Vt", "Rt", "Ot", "ln2_w", "ln2_b", "ftm_k", "ftm_r", "fKt", "fVt", "fRt",
-        "Kf", "Vf", "Rf", "Of", "fKf", "fVf", "fRf")]
+        "Kf", "Vf", "Rf", "Of", "fKf", "fVf", "fRf")] + [("q8", ctypes.POINTER(KrLayerQ8))]
 
 
 class KrModelWeights(ctypes.Structure):

@@ -49,14 +49,15 @@ def workspace(weights, M: int):
     return ws, nbytes
 
 
-def init_weights(model, device: str = "cuda") -> dict:
-    """Prepare weights once per (model, device); `model` has `.w` (rwkv-package
-    keys, [in,out] matrices, raw time_decay) or is such a dict."""
-    key = (id(model), str(device))
+def init_weights(model, device: str = "cuda", w8a8: bool = False) -> dict:
+    """Prepare weights once per (model, device, codec); `model` has `.w`
+    (rwkv-package keys, [in,out] matrices, raw time_decay) or is such a dict.
+    w8a8=True selects the int8 codec (head stays fp16)."""
+    key = (id(model), str(device), bool(w8a8))
     if key in _WEIGHTS_CACHE:
         return _WEIGHTS_CACHE[key]
     w = model.w if hasattr(model, "w") else model
-    P = prepare(w, device)
+    P = prepare(w, device, w8a8=w8a8)
     bundle = {"prepared": P, "n_embd": P.C, "n_att": P.C, "n_ffn": P.F, "n_vocab": P.V,
               "n_layer": P.n_layer, "device": P.device, "model": model}
     _WEIGHTS_CACHE[key] = bundle

@@ -16,6 +16,17 @@ typedef _Float16 kr_half8 __attribute__((ext_vector_type(8)));
 typedef float kr_float4 __attribute__((ext_vector_type(4)));
 typedef int kr_int4 __attribute__((ext_vector_type(4)));
 
+// fp32 -> fp16 with the value first materialised in fp32. Without the empty
+// asm the AMDGPU backend folds fp16(a * b) into one v_fma_mixlo_f16 (a single
+// rounding straight to fp16) even under -ffp-contract=off, and whether it
+// does depends on the surrounding code: two kernels computing the same
+// expression could then round differently. Every fp16 store of a computed
+// value goes through here, so every kernel rounds to fp32, then to fp16.
+__device__ __forceinline__ _Float16 kr_f16(float v) {
+    __asm__ volatile("" : "+v"(v));
+    return (_Float16)v;
+}
+
 // ---------------------------------------------------------------------------
 // Range-coder constants (32-bit state; the coding spec is a 32-bit range coder
 // with E1/E2/E3 renormalisation, krunch_ac/cpu_reference.py:28-33 and
@@ -72,7 +83,6 @@ static inline hipStream_t kr_stream(void* s) { return reinterpret_cast<hipStream
 // Device helpers
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ float kr_h2f(kr_half h) { return (float)h; }
-__device__ __forceinline__ kr_half kr_f2h(float f) { return (kr_half)f; }
 
 // Logistic function, one definition for every kernel that needs it.
 __device__ __forceinline__ float kr_sigmoid(float x) {

@@ -80,3 +80,7 @@ int kr_gemm_launch(const kr_gemm_args& g, int epilogue, hipStream_t stream);
 int kr_gemm_launch_multi(const kr_gemm_args* jobs, const int* epilogues, int njobs,
                          hipStream_t stream);
 
+
+// Per-row symmetric int8 quantisation of an fp16 [M, K] matrix (kr_quant.hip).
+int kr_impl_quantize_rows(const void* x, long long ldx, int M, int K, void* q, float* scales,
+                          int packed, hipStream_t s);

@@ -36,17 +36,17 @@ __device__ __forceinline__ void store_one(const kr_gemm_args& g, int m, int n, f
     if constexpr (EP == KR_EP_F32) {
         reinterpret_cast<float*>(g.out)[o] = acc;
     } else {
-        const float h = (float)(kr_half)acc;
+        const float h = (float)kr_f16(acc);
         float y;
         if constexpr (EP == KR_EP_F16) y = h;
         else if constexpr (EP == KR_EP_SIGMOID) y = kr_sigmoid(h);
         else if constexpr (EP == KR_EP_RELUSQ) { const float r = h > 0.0f ? h : 0.0f; y = r * r; }
         else if constexpr (EP == KR_EP_RESID) y = (float)g.res[o] + h;
         else {
-            const float gh = (float)(kr_half)((float)g.gate[o] * h);
+            const float gh = (float)kr_f16((float)g.gate[o] * h);
             y = (float)g.res[o] + gh;
         }
-        reinterpret_cast<kr_half*>(g.out)[o] = (kr_half)y;
+        reinterpret_cast<kr_half*>(g.out)[o] = kr_f16(y);
     }
 }
 
@@ -399,14 +399,14 @@ __global__ void __launch_bounds__(MAXT) gemm_panel_kernel(kr_gemm_multi mj) {
             kr_half4 h;
             #pragma unroll
             for (int r = 0; r < 4; r++) {
-                const float x = (float)(kr_half)acc[r];
+                const float x = (float)kr_f16(acc[r]);
                 float y;
                 if (ep == KR_EP_F16) y = x;
                 else if (ep == KR_EP_SIGMOID) y = kr_sigmoid(x);
                 else if (ep == KR_EP_RELUSQ) { const float rr = x > 0.0f ? x : 0.0f; y = rr * rr; }
                 else if (ep == KR_EP_RESID) y = (float)rv[r] + x;
-                else y = (float)rv[r] + (float)(kr_half)((float)gv[r] * x);
-                h[r] = (kr_half)y;
+                else y = (float)rv[r] + (float)kr_f16((float)gv[r] * x);
+                h[r] = kr_f16(y);
             }
             kr_half* dst = reinterpret_cast<kr_half*>(g.out) +
                            (g.out_frag ? kr_frag_index(m, nb, g.N) : o);

@@ -90,7 +90,7 @@ __device__ __forceinline__ void layer_norm_row(RowF<G>& r, const CoefH<G>& w, co
         #pragma unroll
         for (int q = 0; q < 4; q++) {
             const float y = (r.v[i][q] - mean) * rstd * (float)w.v[i][q] + (float)b.v[i][q];
-            r.v[i][q] = (float)(kr_half)y;   // activations are fp16
+            r.v[i][q] = (float)kr_f16(y);   // activations are fp16
         }
     }
 }
@@ -101,7 +101,7 @@ __device__ __forceinline__ void store_row(kr_half* __restrict__ p, int lane, con
     for (int i = 0; i < G; i++) {
         kr_half4 h;
         #pragma unroll
-        for (int q = 0; q < 4; q++) h[q] = (kr_half)r.v[i][q];
+        for (int q = 0; q < 4; q++) h[q] = kr_f16(r.v[i][q]);
         *reinterpret_cast<kr_half4*>(p + 256 * i + 4 * lane) = h;
     }
 }
@@ -120,12 +120,47 @@ __device__ __forceinline__ void store_mix(kr_half* __restrict__ out, size_t row,
         #pragma unroll
         for (int q = 0; q < 4; q++) {
             const float m = (float)t[q];
-            h[q] = (kr_half)(cur.v[i][q] * m + prev.v[i][q] * (1.0f - m));
+            h[q] = kr_f16(cur.v[i][q] * m + prev.v[i][q] * (1.0f - m));
         }
         const int col = 256 * i + 4 * lane;
         const size_t o = frag ? kr_frag_index((long long)row, col, C) : row * C + col;
         *reinterpret_cast<kr_half4*>(out + o) = h;
     }
+}
+
+// w8a8: the fp16 mix row quantised per row (symmetric int8, s = max|v| / 127,
+// q = clamp(rint(v / s), -127, 127); the rule of kr_quantize_rows), row-major
+// or fragment-packed for the small-M int8 GEMM.
+template <int G>
+__device__ __forceinline__ void store_mix_q8(int8_t* __restrict__ out, float* __restrict__ scales,
+                                             size_t row, bool frag, const CoefH<G>& tm, int lane,
+                                             const RowF<G>& cur, const RowF<G>& prev) {
+    constexpr int C = 256 * G;
+    float v[G][4];
+    float amax = 0.0f;
+    #pragma unroll
+    for (int i = 0; i < G; i++)
+        #pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const float m = (float)tm.v[i][q];
+            v[i][q] = (float)kr_f16(cur.v[i][q] * m + prev.v[i][q] * (1.0f - m));
+            amax = fmaxf(amax, fabsf(v[i][q]));
+        }
+    for (int o = 32; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
+    const float s = amax > 0.0f ? amax / 127.0f : 1.0f;
+    #pragma unroll
+    for (int i = 0; i < G; i++) {
+        uint32_t w = 0;
+        #pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const float r = fminf(fmaxf(rintf(v[i][q] / s), -127.0f), 127.0f);
+            w |= ((uint32_t)(uint8_t)(int8_t)(int)r) << (8 * q);
+        }
+        const int col = 256 * i + 4 * lane;
+        const size_t o = frag ? kr_frag_index_i8((long long)row, col, C) : row * C + col;
+        *reinterpret_cast<uint32_t*>(out + o) = w;
+    }
+    if (lane == 0) scales[row] = s;
 }
 
 struct LnMixArgs {
@@ -137,6 +172,8 @@ struct LnMixArgs {
     kr_half* state;            // [B, C] shifted-in row for t = 0; rewritten with LN(x[T-1])
     int B, T, run;             // rows per wave
     int frag;                  // mix outputs fragment-packed (small-M GEMM operands)
+    int8_t* q[3];              // w8a8: NMIX int8 outputs instead of out[] (per-row quantised)
+    float* qs[3];              // w8a8: their per-row scales
 };
 
 // One wave per run of `run` consecutive tokens of one stream. The wave that
@@ -182,8 +219,10 @@ __global__ void __launch_bounds__(256) ln_mix_kernel(LnMixArgs a) {
             store_row<G>(a.out[0] + (row0 + t) * C, lane, cur);
         } else {
             #pragma unroll
-            for (int m = 0; m < NMIX; m++)
-                store_mix<G>(a.out[m], row0 + t, a.frag != 0, tm[m], lane, cur, prev);
+            for (int m = 0; m < NMIX; m++) {
+                if (a.q[0]) store_mix_q8<G>(a.q[m], a.qs[m], row0 + t, a.frag != 0, tm[m], lane, cur, prev);
+                else store_mix<G>(a.out[m], row0 + t, a.frag != 0, tm[m], lane, cur, prev);
+            }
             prev = cur;
         }
     }
@@ -217,7 +256,7 @@ __device__ __forceinline__ kr_half wkv_token(WkvState& st, float w, float u, flo
     const float p1 = fmaxf(st.p, ww);
     const float e1 = __expf(st.p - p1), e2 = __expf(ww - p1);
     const float y = (e1 * st.a + e2 * vv) / (e1 * st.b + e2);
-    const kr_half ry = (kr_half)(rr * (float)(kr_half)y);
+    const kr_half ry = kr_f16(rr * (float)kr_f16(y));
     const float ww2 = w + st.p;
     const float p2 = fmaxf(ww2, kk);
     const float f1 = __expf(ww2 - p2), f2 = __expf(kk - p2);
@@ -331,6 +370,9 @@ int launch_ln_mix(int G, const LnMixArgs& a, hipStream_t s) {
 struct Work {
     kr_half *kx, *vx, *rx, *r, *ry, *fkx, *frx, *rf, *kf;
     float *k, *v;
+    // w8a8 operands and their per-row scales
+    int8_t *kx8, *vx8, *rx8, *ry8, *fkx8, *frx8, *kf8;
+    float *kxs, *vxs, *rxs, *rys, *fkxs, *frxs, *kfs;
 };
 
 inline size_t up256(size_t b) { return (b + 255) / 256 * 256; }
@@ -339,7 +381,8 @@ inline size_t up256(size_t b) { return (b + 255) / 256 * 256; }
 size_t work_bytes(long long M, int C, int F) {
     M = kr_frag_rows(M);
     const size_t h = (size_t)M * C * 2, f = (size_t)M * C * 4, kf = (size_t)M * F * 2;
-    return 8 * up256(h) + 2 * up256(f) + up256(kf);
+    const size_t b = (size_t)M * C, bf = (size_t)M * F, sc = (size_t)M * 4;
+    return 8 * up256(h) + 2 * up256(f) + up256(kf) + 6 * up256(b) + up256(bf) + 7 * up256(sc);
 }
 
 Work carve(void* ws, long long M, int C, int F) {
@@ -359,6 +402,11 @@ Work carve(void* ws, long long M, int C, int F) {
     w.k = reinterpret_cast<float*>(take(f));
     w.v = reinterpret_cast<float*>(take(f));
     w.kf = reinterpret_cast<kr_half*>(take((size_t)M * F * 2));
+    int8_t** q8[6] = {&w.kx8, &w.vx8, &w.rx8, &w.ry8, &w.fkx8, &w.frx8};
+    for (auto b : q8) *b = reinterpret_cast<int8_t*>(take((size_t)M * C));
+    w.kf8 = reinterpret_cast<int8_t*>(take((size_t)M * F));
+    float** sc[7] = {&w.kxs, &w.vxs, &w.rxs, &w.rys, &w.fkxs, &w.frxs, &w.kfs};
+    for (auto b : sc) *b = reinterpret_cast<float*>(take((size_t)M * 4));
     return w;
 }
 
@@ -397,8 +445,75 @@ bool use_fragments(const kr_layer_weights& L, long long M) {
     return M <= KR_GEMM_SMALL_M && L.Kf && L.Vf && L.Rf && L.Of && L.fKf && L.fVf && L.fRf;
 }
 
+// w8a8 layer: the same op order with the seven products on
+// int8 MFMA. LN-mix writes its operands quantised per row; the WKV output and
+// the ReLU^2 output are quantised by a row kernel before their products.
+kr_gemm_args gemm_q8(const int8_t* A, const float* sa, int M, int K, const kr_matrix_q8& W,
+                     int N, void* out, bool fr, const kr_half* res = nullptr,
+                     const kr_half* gate = nullptr) {
+    kr_gemm_args g = gemm_args(reinterpret_cast<const kr_half*>(A), M, K, W.q, N, out, res, gate,
+                               W.qf, fr);
+    g.i8 = 1;
+    g.sa = sa;
+    g.sw = W.scale;
+    return g;
+}
+
+int layer_forward_q8(const kr_layer_weights& L, int C, int F, kr_half* x, int B, int T,
+                     const kr_layer_state& st, const Work& w, hipStream_t s) {
+    const kr_layer_q8& Q = *L.q8;
+    const int M = B * T, G = C / 256;
+    const bool fr = M <= KR_GEMM_SMALL_M && Q.K.qf && Q.V.qf && Q.R.qf && Q.O.qf && Q.fK.qf &&
+                    Q.fV.qf && Q.fR.qf;
+    LnMixArgs a{};
+    a.x = x;
+    a.ln_w = H(L.ln1_w);
+    a.ln_b = H(L.ln1_b);
+    a.tm[0] = H(L.tm_k); a.tm[1] = H(L.tm_v); a.tm[2] = H(L.tm_r);
+    a.q[0] = w.kx8; a.q[1] = w.vx8; a.q[2] = w.rx8;
+    a.qs[0] = w.kxs; a.qs[1] = w.vxs; a.qs[2] = w.rxs;
+    a.state = Hm(st.att_xx);
+    a.B = B;
+    a.T = T;
+    a.run = rows_per_run(T);
+    a.frag = fr ? 1 : 0;
+    KR_TRY(launch_ln_mix<3>(G, a, s));
+    {
+        const kr_gemm_args jobs[3] = {gemm_q8(w.kx8, w.kxs, M, C, Q.K, C, w.k, fr),
+                                      gemm_q8(w.vx8, w.vxs, M, C, Q.V, C, w.v, fr),
+                                      gemm_q8(w.rx8, w.rxs, M, C, Q.R, C, w.r, fr)};
+        const int eps[3] = {KR_EP_F32, KR_EP_F32, KR_EP_SIGMOID};
+        KR_TRY(kr_gemm_launch_multi(jobs, eps, 3, s));
+    }
+    {
+        dim3 grid((C + 255) / 256, B);
+        wkv_kernel<<<grid, 256, 0, s>>>(w.k, w.v, w.r, L.decay, L.first, st.aa, st.bb, st.pp,
+                                        w.ry, B, T, C, 0);
+        KR_LAUNCHED();
+    }
+    KR_TRY(kr_impl_quantize_rows(w.ry, C, M, C, w.ry8, w.rys, fr ? 1 : 0, s));
+    KR_TRY(kr_gemm_launch(gemm_q8(w.ry8, w.rys, M, C, Q.O, C, x, fr, x), KR_EP_RESID, s));
+    a.ln_w = H(L.ln2_w);
+    a.ln_b = H(L.ln2_b);
+    a.tm[0] = H(L.ftm_k); a.tm[1] = H(L.ftm_r);
+    a.q[0] = w.fkx8; a.q[1] = w.frx8;
+    a.qs[0] = w.fkxs; a.qs[1] = w.frxs;
+    a.state = Hm(st.ffn_xx);
+    KR_TRY(launch_ln_mix<2>(G, a, s));
+    {
+        const kr_gemm_args jobs[2] = {gemm_q8(w.frx8, w.frxs, M, C, Q.fR, C, w.rf, fr),
+                                      gemm_q8(w.fkx8, w.fkxs, M, C, Q.fK, F, w.kf, fr)};
+        const int eps[2] = {KR_EP_SIGMOID, KR_EP_RELUSQ};
+        KR_TRY(kr_gemm_launch_multi(jobs, eps, 2, s));
+    }
+    KR_TRY(kr_impl_quantize_rows(w.kf, F, M, F, w.kf8, w.kfs, fr ? 1 : 0, s));
+    KR_TRY(kr_gemm_launch(gemm_q8(w.kf8, w.kfs, M, F, Q.fV, C, x, fr, x, w.rf), KR_EP_GATED, s));
+    return KR_OK;
+}
+
 int layer_forward(const kr_layer_weights& L, int C, int F, kr_half* x, int B, int T,
                   const kr_layer_state& st, const Work& w, hipStream_t s) {
+    if (L.q8) return layer_forward_q8(L, C, F, x, B, T, st, w, s);
     const int M = B * T, G = C / 256;
     const bool fr = use_fragments(L, M);
     LnMixArgs a{};

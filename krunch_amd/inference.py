@@ -28,7 +28,8 @@ from krunch_amd.model import State
 
 BLOB_MAGIC = b"KRNC"
 BLOB_VERSION = 1
-MODEL_ID = 1
+MODEL_ID = 1            # fp16 codec
+MODEL_ID_W8A8 = 2       # w8a8 codec (int8 layer products; a different bitstream)
 TOKENIZER_ID = 1
 HEADER_FMT = ">4sBIIIHHQII"
 HEADER_SIZE = struct.calcsize(HEADER_FMT)
@@ -64,16 +65,20 @@ class InferenceEngine:
         # lockstep streams may be split into concurrent groups (graph branches); one
         # group measured fastest on MI355X (branches of one graph do not overlap)
         self.decode_groups = int(os.environ.get("KRUNCH_DECODE_GROUPS", "1"))
+        self.model_id = MODEL_ID
 
     # ------------------------------------------------------------------ setup
     def load(self, weights: Optional[dict] = None, tokenizer_path: Optional[str] = None,
-             device: str = "cuda"):
+             device: str = "cuda", w8a8: bool = False):
         """Prepare weights (a dict in the rwkv-package layout; default: the
-        synthetic RWKV-4-169M-shaped model, seed 0) and an optional tokenizer."""
+        synthetic RWKV-4-169M-shaped model, seed 0) and an optional tokenizer.
+        w8a8=True selects the int8 codec (model_id 2): its streams decode only
+        with the int8 codec."""
         if weights is None:
             from krunch_amd.synthetic import make_weights
             weights = make_weights()
-        self._weights = cpp_path.init_weights(weights, device)
+        self._weights = cpp_path.init_weights(weights, device, w8a8=w8a8)
+        self.model_id = MODEL_ID_W8A8 if w8a8 else MODEL_ID
         if tokenizer_path:
             from tokenizers import Tokenizer
             self._tokenizer = Tokenizer.from_file(str(tokenizer_path))

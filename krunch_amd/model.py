@@ -40,6 +40,20 @@ def _fragments(Wt: torch.Tensor) -> torch.Tensor:
     return out
 
 
+def _quantized(Wt: torch.Tensor):
+    """w8a8 copy of Wt [N, K]: int8 rows (one fp32 scale per output channel,
+    kr_quantize_rows) and their fragment-packed copy for the small-M GEMM."""
+    N, K = Wt.shape
+    q = torch.empty((N, K), dtype=torch.int8, device=Wt.device)
+    scale = torch.empty(N, dtype=torch.float32, device=Wt.device)
+    _lib.call("kr_quantize_rows", Wt.data_ptr(), K, N, K, q.data_ptr(), scale.data_ptr(), 0,
+              _lib.stream_ptr())
+    qf = torch.empty(_lib.lib().kr_fragment_bytes(N, K // 2), dtype=torch.int8, device=Wt.device)
+    _lib.call("kr_pack_fragments", q.data_ptr(), K // 2, N, K // 2, qf.data_ptr(),
+              _lib.stream_ptr())
+    return q, qf, scale
+
+
 def _transposed(W: torch.Tensor, device) -> torch.Tensor:
     """[K, N] -> [N, K] fp16 on the device via kr_transpose_f16."""
     src = W.to(device=device, dtype=torch.float16).contiguous()
@@ -59,6 +73,8 @@ class Prepared:
     tensors: dict = field(default_factory=dict)
     layers_c: object = None
     model_c: object = None
+    w8a8: bool = False
+    q8_c: object = None
 
     @property
     def ptr(self):
@@ -68,12 +84,14 @@ class Prepared:
         return ctypes.byref(self.layers_c[i])
 
 
-def prepare(w: dict, device=None) -> Prepared:
+def prepare(w: dict, device=None, w8a8: bool = False) -> Prepared:
+    """w8a8=True also builds the int8 codec's weights: the
+    seven layer matrices quantised per output channel; the head stays fp16."""
     device = _dev(device)
     n_layer = 1 + max(int(k.split(".")[1]) for k in w if k.startswith("blocks."))
     V, C = w["emb.weight"].shape
     F = w["blocks.0.ffn.key.weight"].shape[1]
-    P = Prepared(n_layer, C, F, V, device)
+    P = Prepared(n_layer, C, F, V, device, w8a8=w8a8)
     t = P.tensors
     h = lambda x: x.to(device=device, dtype=torch.float16).reshape(-1).contiguous()
     t["emb"] = w["emb.weight"].to(device=device, dtype=torch.float16).contiguous()
@@ -99,9 +117,23 @@ def prepare(w: dict, device=None) -> Prepared:
         L["fRt"] = _transposed(w[f + "receptance.weight"], device)
         for src in ("K", "V", "R", "O", "fK", "fV", "fR"):
             L[src + "f"] = _fragments(L[src + "t"])
+        if w8a8:
+            for src in ("K", "V", "R", "O", "fK", "fV", "fR"):
+                L[src + "_q"], L[src + "_qf"], L[src + "_qs"] = _quantized(L[src + "t"])
         for name, tensor in L.items():
             t[f"{i}.{name}"] = tensor
-            setattr(layers[i], name, tensor.data_ptr())
+            if "_q" not in name:
+                setattr(layers[i], name, tensor.data_ptr())
+    if w8a8:
+        q8 = (_lib.KrLayerQ8 * n_layer)()
+        for i in range(n_layer):
+            for src in ("K", "V", "R", "O", "fK", "fV", "fR"):
+                m = getattr(q8[i], src)
+                m.q = t[f"{i}.{src}_q"].data_ptr()
+                m.qf = t[f"{i}.{src}_qf"].data_ptr()
+                m.scale = t[f"{i}.{src}_qs"].data_ptr()
+            layers[i].q8 = ctypes.pointer(q8[i])
+        P.q8_c = q8
     P.layers_c = layers
     P.model_c = _lib.KrModelWeights(n_layer, C, F, V, t["emb"].data_ptr(), t["ln_out_w"].data_ptr(),
                                     t["ln_out_b"].data_ptr(), t["headT"].data_ptr(),

@@ -35,7 +35,20 @@ def new_state(n_layer: int, B: int, C: int):
             for _ in range(n_layer)]
 
 
-def _mm(x: torch.Tensor, w: torch.Tensor, rowwise: bool) -> torch.Tensor:
+def _mm_q8(x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
+    """w8a8 product (oracle/quant.py): x quantised per row, w [in, out] per
+    output channel, exact integer sums, two float32 scale multiplies."""
+    from oracle import quant
+    qw, sw = quant.quantize_rows(w.t().contiguous().numpy())
+    flat = x.reshape(-1, x.shape[-1]).numpy()
+    qa, sa = quant.quantize_rows(flat)
+    y = torch.from_numpy(quant.matmul_i8(qa, sa, qw, sw))
+    return y.reshape(*x.shape[:-1], w.shape[-1])
+
+
+def _mm(x: torch.Tensor, w: torch.Tensor, rowwise: bool, q8: bool = False) -> torch.Tensor:
+    if q8:
+        return _mm_q8(x, w)
     if not rowwise:
         return x @ w
     flat = x.reshape(-1, x.shape[-1])
@@ -70,7 +83,7 @@ def _f32(t):
     return t.to(torch.float32)
 
 
-def time_mix(x, st, w, i, rowwise):
+def time_mix(x, st, w, i, rowwise, q8=False):
     a, b = f"blocks.{i}.att.", f"blocks.{i}."
     C = x.shape[-1]
     xx = F.layer_norm(x, (C,), _f32(w[b + "ln1.weight"]), _f32(w[b + "ln1.bias"]), LN_EPS)
@@ -79,16 +92,16 @@ def time_mix(x, st, w, i, rowwise):
     kx = xx * mk + sx * (1 - mk)
     vx = xx * mv + sx * (1 - mv)
     rx = xx * mr + sx * (1 - mr)
-    r = torch.sigmoid(_mm(rx, _f32(w[a + "receptance.weight"]), rowwise))
-    k = _mm(kx, _f32(w[a + "key.weight"]), rowwise)
-    v = _mm(vx, _f32(w[a + "value.weight"]), rowwise)
+    r = torch.sigmoid(_mm(rx, _f32(w[a + "receptance.weight"]), rowwise, q8))
+    k = _mm(kx, _f32(w[a + "key.weight"]), rowwise, q8)
+    v = _mm(vx, _f32(w[a + "value.weight"]), rowwise, q8)
     decay = -torch.exp(_f32(w[a + "time_decay"]).reshape(C))
     y = wkv(k, v, decay, _f32(w[a + "time_first"]).reshape(C), st)
     st["att_xx"] = xx[:, -1, :].clone()
-    return x + _mm(r * y, _f32(w[a + "output.weight"]), rowwise)
+    return x + _mm(r * y, _f32(w[a + "output.weight"]), rowwise, q8)
 
 
-def channel_mix(x, st, w, i, rowwise):
+def channel_mix(x, st, w, i, rowwise, q8=False):
     f, b = f"blocks.{i}.ffn.", f"blocks.{i}."
     C = x.shape[-1]
     xx = F.layer_norm(x, (C,), _f32(w[b + "ln2.weight"]), _f32(w[b + "ln2.bias"]), LN_EPS)
@@ -96,22 +109,25 @@ def channel_mix(x, st, w, i, rowwise):
     mk, mr = (_f32(w[f + n]).reshape(C) for n in ("time_mix_k", "time_mix_r"))
     kx = xx * mk + sx * (1 - mk)
     rx = xx * mr + sx * (1 - mr)
-    r = torch.sigmoid(_mm(rx, _f32(w[f + "receptance.weight"]), rowwise))
-    kk = torch.relu(_mm(kx, _f32(w[f + "key.weight"]), rowwise)) ** 2
+    r = torch.sigmoid(_mm(rx, _f32(w[f + "receptance.weight"]), rowwise, q8))
+    kk = torch.relu(_mm(kx, _f32(w[f + "key.weight"]), rowwise, q8)) ** 2
     st["ffn_xx"] = xx[:, -1, :].clone()
-    return x + r * _mm(kk, _f32(w[f + "value.weight"]), rowwise)
+    return x + r * _mm(kk, _f32(w[f + "value.weight"]), rowwise, q8)
 
 
-def forward(w: dict, ids: torch.Tensor, state, rowwise: bool = False) -> torch.Tensor:
-    """ids [B, T] int -> logits [B, T, V] fp32; mutates `state` (list per layer)."""
+def forward(w: dict, ids: torch.Tensor, state, rowwise: bool = False,
+            w8a8: bool = False) -> torch.Tensor:
+    """ids [B, T] int -> logits [B, T, V] fp32; mutates `state` (list per layer).
+    w8a8=True runs the seven layer products as the int8 codec defines them
+    (oracle/quant.py); the head stays floating point."""
     ids = torch.as_tensor(ids, dtype=torch.long)
     if ids.dim() == 1:
         ids = ids.unsqueeze(0)
     x = _f32(w["emb.weight"])[ids]
     with torch.no_grad():
         for i, st in enumerate(state):
-            x = time_mix(x, st, w, i, rowwise)
-            x = channel_mix(x, st, w, i, rowwise)
+            x = time_mix(x, st, w, i, rowwise, w8a8)
+            x = channel_mix(x, st, w, i, rowwise, w8a8)
         C = x.shape[-1]
         x = F.layer_norm(x, (C,), _f32(w["ln_out.weight"]), _f32(w["ln_out.bias"]), LN_EPS)
         return _mm(x, _f32(w["head.weight"]), rowwise)
