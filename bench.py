@@ -43,6 +43,8 @@ def parse():
     ap.add_argument("--cpu-decode-steps", type=int, default=48)
     ap.add_argument("--groups", type=int, default=1,
                     help="decode the B streams as this many concurrent groups (graph branches)")
+    ap.add_argument("--no-w8a8", action="store_true",
+                    help="skip the w8a8 codec (BASELINE config 4) run on the same windows")
     ap.add_argument("--kernel-probe", action="store_true",
                     help="only run a 256 MiB device copy (counter calibration) and 8 launches of "
                          "the dominant kernel, for rocprofv3 --pmc runs")
@@ -76,14 +78,14 @@ def kernel_probe(weights16, B):
     print(json.dumps({"probe": "ok", "copy_bytes": 2 * src.numel() * 4}))
 
 
-def gpu_bench(args, weights16):
+def gpu_bench(args, weights16, w8a8=False):
     import numpy as np
     import torch
     from krunch_amd import _lib, cpp_path, synthetic
     from krunch_amd.model import State
 
     dev = torch.device("cuda")
-    W = cpp_path.init_weights(weights16, "cuda")
+    W = cpp_path.init_weights(weights16, "cuda", w8a8=w8a8)
     P = W["prepared"]
     B, Tw = args.batch, args.window
     n_win = args.warmup + args.steps
@@ -344,6 +346,24 @@ def main():
         "bits_per_token": round(8 * r["comp_bytes"] / r["total_tok"], 4),
         "roundtrip_exact": r["exact"],
     }
+    if not args.no_w8a8:
+        # the w8a8 codec (int8 MFMA layer products, fp16 head)
+        # on the same windows; its bits/token beside the fp16 codec's.
+        q = gpu_bench(args, weights16, w8a8=True)
+        qkb = q["ntok"] * BYTES_PER_TOKEN / 1024
+        bpt16 = 8 * r["comp_bytes"] / r["total_tok"]
+        bpt8 = 8 * q["comp_bytes"] / q["total_tok"]
+        res["w8a8"] = {
+            "compress_kbps": round(qkb / q["t_c"], 2),
+            "compress_tok_s": round(q["ntok"] / q["t_c"], 1),
+            "decompress_kbps": round(qkb / q["t_d"], 2),
+            "roundtrip_kbps": round(qkb / (q["t_c"] + q["t_d"]), 2),
+            "bits_per_token": round(bpt8, 6),
+            "bits_per_token_fp16": round(bpt16, 6),
+            "bits_delta_pct_vs_fp16": round(100 * (bpt8 - bpt16) / bpt16, 5),
+            "roundtrip_exact": q["exact"],
+            "compress_int8_fp16_tops": round(q["ntok"] * FLOP_PER_TOKEN / q["t_c"] / 1e12, 1),
+        }
     res["roofline"] = dominant_kernel_roofline(weights16, args.batch)
     if not args.no_cpu_baseline:
         res["cpu_baseline"] = cpu_baseline(weights16, args)
