@@ -12,12 +12,16 @@ carried across windows (inference.py:311-338, generalised from one chunk to B
 chunks per call); `decompress_tokens_batched` decodes B chunks in lockstep,
 one token per stream per step, with the CDF search and range decode fused on
 the GPU and the whole step replayed from one HIP graph (inference.py:363-443).
-Byte-level methods tokenize with a `tokenizers` JSON when one is loaded.
+Byte-level methods tokenize with a `tokenizers` JSON when one is loaded,
+else with the byte tokenizer (krunch_amd/tokenizer.py); `compress` /
+`decompress` write and read the `.krunch` container (cli.py:49-118,
+chunking.py) with CRC32, length and codec checks.
 """
 from __future__ import annotations
 
 import os
 import struct
+import zlib
 from typing import List, Optional, Sequence
 
 import numpy as np
@@ -38,8 +42,9 @@ CDF_PRECISION = 24
 
 
 def encode_header(original_len: int, n_chunks: int, crc32: int, adapter_id: int = 0,
-                  adapter_version: int = 0, flags: int = 0, model_id: int = MODEL_ID) -> bytes:
-    return struct.pack(HEADER_FMT, BLOB_MAGIC, BLOB_VERSION, model_id, TOKENIZER_ID, adapter_id,
+                  adapter_version: int = 0, flags: int = 0, model_id: int = MODEL_ID,
+                  tokenizer_id: int = TOKENIZER_ID) -> bytes:
+    return struct.pack(HEADER_FMT, BLOB_MAGIC, BLOB_VERSION, model_id, tokenizer_id, adapter_id,
                        adapter_version, flags, original_len, n_chunks, crc32)
 
 
@@ -79,11 +84,15 @@ class InferenceEngine:
             weights = make_weights()
         self._weights = cpp_path.init_weights(weights, device, w8a8=w8a8)
         self.model_id = MODEL_ID_W8A8 if w8a8 else MODEL_ID
-        if tokenizer_path:
-            from tokenizers import Tokenizer
-            self._tokenizer = Tokenizer.from_file(str(tokenizer_path))
+        from krunch_amd.tokenizer import load_tokenizer
+        self._tokenizer = load_tokenizer(tokenizer_path)
         self._ready = True
         return self
+
+    @property
+    def tokenizer_id(self) -> int:
+        """1 for a tokenizers JSON (the reference's id), 0 for the byte tokenizer."""
+        return self._tokenizer.tokenizer_id if self._tokenizer is not None else TOKENIZER_ID
 
     @property
     def ready(self) -> bool:
@@ -205,17 +214,18 @@ class InferenceEngine:
         return [host[b, :n_tok[b]].copy() for b in range(B)]
 
     # ------------------------------------------------------------ byte level
+    # inference.py:203-230,483-497,576-747: chunk bytes -> tokens -> payload
+    # (`>II` orig_len, n_tokens + bits) and back, B chunks per batched call.
     def _need_tokenizer(self):
         if self._tokenizer is None:
-            raise RuntimeError("byte-level API needs a tokenizer: load(tokenizer_path=...)")
+            raise RuntimeError("call load() first")
 
     def compress_chunk(self, data: bytes) -> bytes:
         return self.compress_chunks_batched([data])[0]
 
     def compress_chunks_batched(self, chunks: Sequence[bytes]) -> List[bytes]:
         self._need_tokenizer()
-        toks = [np.array(self._tokenizer.encode(c.decode("utf-8", errors="replace")).ids,
-                         dtype=np.int32) for c in chunks]
+        toks = [self._tokenizer.encode_bytes(c) for c in chunks]
         return self.compress_tokens_batched(toks, orig_lens=[len(c) for c in chunks])
 
     def decompress_chunk(self, encoded: bytes) -> bytes:
@@ -227,8 +237,41 @@ class InferenceEngine:
         out = []
         for enc, t in zip(encoded_chunks, toks):
             orig_len, _ = struct.unpack(">II", enc[:8])
-            out.append(self._tokenizer.decode(t.tolist()).encode("utf-8")[:orig_len])
+            out.append(self._tokenizer.decode_bytes(t)[:orig_len])
         return out
+
+    # ------------------------------------------------------------- container
+    def compress(self, raw: bytes, chunk_size: Optional[int] = None) -> bytes:
+        """bytes -> .krunch blob: header (model_id, tokenizer_id, length,
+        chunk count, CRC32) + one `>II`(orig_len, comp_len) entry per chunk
+        (cli.py:49-70, chunking.py:88-111); all chunks in one batched call."""
+        from krunch_amd import chunking
+        entries, n = chunking.compress_all(raw, self.compress_chunk,
+                                           neural_batch_fn=self.compress_chunks_batched,
+                                           chunk_size=chunk_size)
+        crc = zlib.crc32(raw) & 0xFFFFFFFF
+        return encode_header(len(raw), n, crc, model_id=self.model_id,
+                             tokenizer_id=self.tokenizer_id) + b"".join(entries)
+
+    def decompress(self, blob: bytes) -> bytes:
+        """.krunch blob -> bytes, all chunks decoded in lockstep; checks the
+        codec (model_id / tokenizer_id), the CRC32 unless flags bit 0 says
+        there is none, and the length (cli.py:73-118)."""
+        from krunch_amd import chunking
+        hdr = decode_header(blob)
+        if hdr["model_id"] != self.model_id:
+            raise ValueError(f"blob model_id {hdr['model_id']} != loaded codec {self.model_id}")
+        if hdr["tokenizer_id"] != self.tokenizer_id:
+            raise ValueError(f"blob tokenizer_id {hdr['tokenizer_id']} != loaded {self.tokenizer_id}")
+        raw = chunking.decompress_all(blob[HEADER_SIZE:], hdr["n_chunks"], self.decompress_chunk,
+                                      neural_batch_fn=self.decompress_chunks_batched)
+        if not hdr["flags"] & 0x01:
+            actual = zlib.crc32(raw) & 0xFFFFFFFF
+            if actual != hdr["crc32"]:
+                raise ValueError(f"CRC32 mismatch: got {actual:#010x}, expected {hdr['crc32']:#010x}")
+        if len(raw) != hdr["original_len"]:
+            raise ValueError(f"length mismatch: got {len(raw)}, expected {hdr['original_len']}")
+        return raw
 
 
 engine = InferenceEngine()
