@@ -307,6 +307,150 @@ __global__ void __launch_bounds__(256) wkv_kernel(const float* __restrict__ k,
     pp[s] = st.p;
 }
 
+// ---------------------------------------------------------------------------
+// Stepped K, V, R products fused with the WKV update (T = 1 rows): the three
+// small-M products and wkv_kernel in one launch, with the arithmetic of the
+// unfused sequence (split-K slices folded in order; k, v fp32; r =
+// fp16(sigmoid(fp16(acc))); wkv_token), so the bits are those of the packed
+// path.
+//
+// One workgroup per (16*TM rows) x (16*NS columns) tile of all three
+// products, 3*S waves (S = C/256 K slices): wave (j, s) loads its slice of
+// the fragment-packed mix operand of product j and of the weight panels and
+// runs the MFMA chains. The slice partials meet in LDS, and the waves then
+// fold (k, v, r) of each 16 x 16 tile and apply WKV, updating the state in
+// place and writing ry fragment-packed for the output projection. k, v and r
+// never leave the CU; the WKV operands of a tile are copied into LDS while
+// the products run.
+// ---------------------------------------------------------------------------
+struct KvrWkvArgs {
+    const kr_half* A[3];       // mixes for K, V, R: fragment-packed [M16, C]
+    const kr_half* Wf[3];      // K, V, R weights, W^T fragment-packed ([C, C])
+    const float* decay;        // [C] time decay (already -exp)
+    const float* first;        // [C] time first
+    float* aa;                 // [M, C] WKV state, updated in place
+    float* bb;
+    float* pp;
+    kr_half* ry;               // fragment-packed [M16, C] (K = C operand of the output GEMM)
+    int M;
+};
+
+// Asynchronous 16-byte copy global -> LDS (lane l writes lds_base + 16 l);
+// counted in vmcnt like a load, no VGPRs held.
+__device__ __forceinline__ void lds_dma16(const void* src, void* lds_base) {
+    __builtin_amdgcn_global_load_lds(
+        (const __attribute__((address_space(1))) void*)src,
+        (__attribute__((address_space(3))) void*)lds_base, 16, 0, 0);
+}
+
+template <int S, int TM, int NS>
+__global__ void __launch_bounds__(192 * S) kvr_wkv_kernel(KvrWkvArgs a) {
+    constexpr int C = 256 * S, NW = 3 * S, TT = TM * NS;
+    constexpr int KB = C / 32;                        // 1 KB blocks per fragment row
+    __shared__ __attribute__((aligned(16))) float part[3 * S * TT * 256];   // slice partials
+    __shared__ __attribute__((aligned(16))) char wk[TT * 5 * 1024];         // WKV operands
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int j = wave / S, s = wave % S;
+    const int M = a.M;
+    // tile; the column groups are dealt so that one group's weight panels
+    // stay on one XCD (workgroups go to the 8 XCDs round robin)
+    constexpr int ng = C / (16 * NS);
+    const int mt = (M + 16 * TM - 1) / (16 * TM);
+    int m_t, n_g;
+    if constexpr ((ng & 7) == 0) {
+        const int k = blockIdx.x >> 3;
+        n_g = (k / mt) * 8 + (blockIdx.x & 7);
+        m_t = k % mt;
+    } else {
+        m_t = blockIdx.x / ng;
+        n_g = blockIdx.x % ng;
+    }
+    const int m0 = m_t * 16 * TM, n0 = n_g * 16 * NS;
+    const int last_mb = (M - 1) >> 4;
+
+    // ---- operands of product j over slice s, then the WKV operands into LDS
+    const kr_half* Aj = j == 0 ? a.A[0] : (j == 1 ? a.A[1] : a.A[2]);
+    const kr_half* Wf = j == 0 ? a.Wf[0] : (j == 1 ? a.Wf[1] : a.Wf[2]);
+    kr_half8 av[TM][8], b[NS][8];
+    #pragma unroll
+    for (int i = 0; i < TM; i++) {
+        const kr_half* ap = Aj + ((size_t)min((m0 >> 4) + i, last_mb) * KB + 8 * s) * 512 + lane * 8;
+        #pragma unroll
+        for (int q = 0; q < 8; q++) av[i][q] = *reinterpret_cast<const kr_half8*>(ap + 512 * q);
+    }
+    #pragma unroll
+    for (int t = 0; t < NS; t++) {
+        const kr_half* bp = Wf + ((size_t)((n0 >> 4) + t) * KB + 8 * s) * 512 + lane * 8;
+        #pragma unroll
+        for (int q = 0; q < 8; q++) b[t][q] = *reinterpret_cast<const kr_half8*>(bp + 512 * q);
+    }
+    // in tile t a lane owns row tile_m(t), columns tile_n(t) .. +3
+    auto tile_m = [&](int t) { return m0 + 16 * (t / NS) + (lane & 15); };
+    auto tile_n = [&](int t) { return n0 + 16 * (t % NS) + 4 * (lane >> 4); };
+    for (int t = wave; t < TT; t += NW) {
+        const int en = tile_n(t);
+        const size_t o = (size_t)min(tile_m(t), M - 1) * C + en;
+        char* d = wk + t * 5 * 1024;
+        lds_dma16(a.aa + o, d);
+        lds_dma16(a.bb + o, d + 1024);
+        lds_dma16(a.pp + o, d + 2048);
+        lds_dma16(a.decay + en, d + 3072);
+        lds_dma16(a.first + en, d + 4096);
+    }
+
+    // ---- MFMA chains (weight fragment in the A slot: lanes hold 4 columns of a row)
+    #pragma unroll
+    for (int i = 0; i < TM; i++)
+        #pragma unroll
+        for (int t = 0; t < NS; t++) {
+            kr_float4 acc = kr_float4{0.f, 0.f, 0.f, 0.f};
+            #pragma unroll
+            for (int q = 0; q < 8; q++)
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(b[t][q], av[i][q], acc, 0, 0, 0);
+            *reinterpret_cast<kr_float4*>(part + ((j * S + s) * TT + i * NS + t) * 256 + lane * 4) = acc;
+        }
+    // the WKV copies of every wave must have landed before the barrier
+    __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+
+    // ---- fold the slices in order, then WKV on (k, v, r) of each tile
+    for (int t = wave; t < TT; t += NW) {
+        const int em = tile_m(t), en = tile_n(t);
+        if (em >= M) continue;
+        auto fold = [&](int jj) {
+            kr_float4 v = *reinterpret_cast<const kr_float4*>(part + (jj * S * TT + t) * 256 + lane * 4);
+            #pragma unroll
+            for (int q = 1; q < S; q++)
+                v = v + *reinterpret_cast<const kr_float4*>(part + ((jj * S + q) * TT + t) * 256 + lane * 4);
+            return v;
+        };
+        const kr_float4 k = fold(0), v = fold(1), rv = fold(2);
+        const char* d = wk + t * 5 * 1024 + 16 * lane;
+        kr_float4 sa = *reinterpret_cast<const kr_float4*>(d);
+        kr_float4 sb = *reinterpret_cast<const kr_float4*>(d + 1024);
+        kr_float4 sp = *reinterpret_cast<const kr_float4*>(d + 2048);
+        const kr_float4 dw = *reinterpret_cast<const kr_float4*>(d + 3072);
+        const kr_float4 du = *reinterpret_cast<const kr_float4*>(d + 4096);
+        kr_half4 ry;
+        #pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const float r = (float)kr_f16(kr_sigmoid((float)kr_f16(rv[e])));
+            WkvState st{sa[e], sb[e], sp[e]};
+            ry[e] = wkv_token(st, dw[e], du[e], k[e], v[e], r);
+            sa[e] = st.a;
+            sb[e] = st.b;
+            sp[e] = st.p;
+        }
+        const size_t o = (size_t)em * C + en;
+        *reinterpret_cast<kr_float4*>(a.aa + o) = sa;
+        *reinterpret_cast<kr_float4*>(a.bb + o) = sb;
+        *reinterpret_cast<kr_float4*>(a.pp + o) = sp;
+        *reinterpret_cast<kr_half4*>(a.ry + kr_frag_index(em, en, C)) = ry;
+    }
+}
+
 // x[row] = emb[ids[row]] (ids clamped into [0, V) so a bad id cannot read
 // out of bounds; callers validate ids before upload).
 template <int G>
@@ -364,6 +508,48 @@ int launch_ln_mix(int G, const LnMixArgs& a, hipStream_t s) {
     }
     KR_LAUNCHED();
     return KR_OK;
+}
+
+// Tile shape of the fused K, V, R + WKV launch: the fewest operand lines on
+// the busiest CU (workgroups spread over 256 CUs, each reading 3 x (16*TM +
+// 16*NS) rows of C), ties to more workgroups.
+template <int S, int TM, int NS>
+int launch_kvr_wkv_shape(const KvrWkvArgs& a, hipStream_t s) {
+    const int mt = (a.M + 16 * TM - 1) / (16 * TM);
+    const int blocks = mt * (256 * S / (16 * NS));
+    kvr_wkv_kernel<S, TM, NS><<<blocks, 192 * S, 0, s>>>(a);
+    KR_LAUNCHED();
+    return KR_OK;
+}
+
+template <int S>
+int launch_kvr_wkv_s(const KvrWkvArgs& a, hipStream_t s) {
+    const int shapes[4][2] = {{2, 2}, {2, 1}, {1, 2}, {1, 1}};
+    long long best = -1;
+    int bi = 0;
+    for (int i = 0; i < 4; i++) {
+        const int TM = shapes[i][0], NS = shapes[i][1];
+        const long long wgs = (long long)((a.M + 16 * TM - 1) / (16 * TM)) * (256 * S / (16 * NS));
+        const long long cost = ((wgs + 255) / 256) * (TM + NS) * 4096 - std::min(wgs, 256ll);
+        if (best < 0 || cost < best) { best = cost; bi = i; }
+    }
+    switch (bi) {
+        case 0: return launch_kvr_wkv_shape<S, 2, 2>(a, s);
+        case 1: return launch_kvr_wkv_shape<S, 2, 1>(a, s);
+        case 2: return launch_kvr_wkv_shape<S, 1, 2>(a, s);
+        default: return launch_kvr_wkv_shape<S, 1, 1>(a, s);
+    }
+}
+
+int launch_kvr_wkv(int G, const KvrWkvArgs& a, hipStream_t s) {
+    if (a.M == 0) return KR_OK;
+    switch (G) {
+        case 1: return launch_kvr_wkv_s<1>(a, s);
+        case 2: return launch_kvr_wkv_s<2>(a, s);
+        case 3: return launch_kvr_wkv_s<3>(a, s);
+        case 4: return launch_kvr_wkv_s<4>(a, s);
+        default: return kr_fail(KR_EUNSUPPORTED, "C=%d unsupported (256..1024, step 256)", 256 * G);
+    }
 }
 
 // Workspace carve-up for M rows.
@@ -511,11 +697,59 @@ int layer_forward_q8(const kr_layer_weights& L, int C, int F, kr_half* x, int B,
     return KR_OK;
 }
 
+// Stepped (T = 1) fp16 layer with fragment-packed weights: LN1-mix, the
+// K, V, R products fused with WKV, the output projection, LN2-mix and the
+// channel mix (six launches).
+int layer_step_fused(const kr_layer_weights& L, int C, int F, kr_half* x, int B,
+                     const kr_layer_state& st, const Work& w, hipStream_t s) {
+    const int M = B, G = C / 256;
+    LnMixArgs a{};
+    a.x = x;
+    a.ln_w = H(L.ln1_w);
+    a.ln_b = H(L.ln1_b);
+    a.tm[0] = H(L.tm_k); a.tm[1] = H(L.tm_v); a.tm[2] = H(L.tm_r);
+    a.out[0] = w.kx; a.out[1] = w.vx; a.out[2] = w.rx;
+    a.state = Hm(st.att_xx);
+    a.B = B;
+    a.T = 1;
+    a.run = 1;
+    a.frag = 1;
+    KR_TRY(launch_ln_mix<3>(G, a, s));
+    KvrWkvArgs kw{};
+    kw.A[0] = w.kx; kw.A[1] = w.vx; kw.A[2] = w.rx;
+    kw.Wf[0] = H(L.Kf); kw.Wf[1] = H(L.Vf); kw.Wf[2] = H(L.Rf);
+    kw.decay = L.decay;
+    kw.first = L.first;
+    kw.aa = st.aa;
+    kw.bb = st.bb;
+    kw.pp = st.pp;
+    kw.ry = w.ry;
+    kw.M = M;
+    KR_TRY(launch_kvr_wkv(G, kw, s));
+    KR_TRY(kr_gemm_launch(gemm_args(w.ry, M, C, L.Ot, C, x, x, nullptr, L.Of, true), KR_EP_RESID, s));
+    a.ln_w = H(L.ln2_w);
+    a.ln_b = H(L.ln2_b);
+    a.tm[0] = H(L.ftm_k); a.tm[1] = H(L.ftm_r);
+    a.out[0] = w.fkx; a.out[1] = w.frx;
+    a.state = Hm(st.ffn_xx);
+    KR_TRY(launch_ln_mix<2>(G, a, s));
+    {
+        const kr_gemm_args jobs[2] = {
+            gemm_args(w.frx, M, C, L.fRt, C, w.rf, nullptr, nullptr, L.fRf, true),
+            gemm_args(w.fkx, M, C, L.fKt, F, w.kf, nullptr, nullptr, L.fKf, true, true)};
+        const int eps[2] = {KR_EP_SIGMOID, KR_EP_RELUSQ};
+        KR_TRY(kr_gemm_launch_multi(jobs, eps, 2, s));
+    }
+    KR_TRY(kr_gemm_launch(gemm_args(w.kf, M, F, L.fVt, C, x, x, w.rf, L.fVf, true), KR_EP_GATED, s));
+    return KR_OK;
+}
+
 int layer_forward(const kr_layer_weights& L, int C, int F, kr_half* x, int B, int T,
                   const kr_layer_state& st, const Work& w, hipStream_t s) {
     if (L.q8) return layer_forward_q8(L, C, F, x, B, T, st, w, s);
     const int M = B * T, G = C / 256;
     const bool fr = use_fragments(L, M);
+    if (fr && T == 1) return layer_step_fused(L, C, F, x, B, st, w, s);
     LnMixArgs a{};
     a.x = x;
     a.ln_w = H(L.ln1_w);
