@@ -212,6 +212,235 @@ __global__ void __launch_bounds__(256, 2) gemm_tile_kernel(kr_gemm_args g) {
 }
 
 // ---------------------------------------------------------------------------
+// Wide tile kernel (large M, fp16)
+// ---------------------------------------------------------------------------
+
+// 256 x 128 output tile per workgroup of 8 waves (4 x 2), each wave 64 x 64 =
+// 4 x 4 MFMA tiles. Time on MI355X is set by the L2 lines a CU has in flight
+// (about 64 at ~470 cycles), so the tile is as large as the registers allow
+// (the 256-wide slice partials and the running total both stay in
+// registers): per 64-wide K step a CU fetches 384 lines for 2M MACs, where the
+// 128 x 128 kernel fetches 512 lines for the same MACs at two workgroups per
+// CU. With one workgroup per CU the loads must run ahead of the MFMAs: both
+// operands go global -> LDS by asynchronous copies (no registers held) into a
+// 3-stage ring, two K steps ahead of the step being multiplied, with one
+// barrier per step.
+//
+// The copies are issued as inline assembly with explicit vmcnt waits: the
+// compiler's own tracking of LDS copies waits for all of them before any LDS
+// read, which would serialise the ring. Nothing else in the loop touches
+// vector memory, so the counts are exact: 6 copies per wave per K step.
+//
+// LDS layout of a stage (16-byte units): row r, 8-wide k chunk kc at
+// 64 (r / 8) + 8 (r % 8) + (kc ^ ((r / 2) % 8)). One copy instruction fills
+// 64 consecutive units = 8 whole rows (8 full 128-byte lines of the operand);
+// an MFMA fragment read (16 rows, one chunk) hits 16 distinct bank groups.
+// The weight fragment takes the MFMA's A slot, so a lane ends with 4
+// consecutive columns of one row (vector stores); every output element is
+// still the 8-deep chain per 256-wide slice folded in order, the bits of the
+// other kernels.
+constexpr int kBigM = 256, kBigN = 128;
+constexpr int kBigStage = (kBigM + kBigN) * 8;   // 16-byte units per stage (48 KB)
+
+__device__ __forceinline__ int big_pos(int r, int kc) {
+    return 64 * (r >> 3) + 8 * (r & 7) + (kc ^ ((r >> 1) & 7));
+}
+
+// 16-byte asynchronous copy global -> LDS: lane l writes LDS byte address
+// lds + 16 l. Invisible to the compiler's wait-count tracking (see above).
+__device__ __forceinline__ void big_copy(const void* src, unsigned lds) {
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off"
+                 :: "s"(lds), "v"(src) : "memory", "m0");
+}
+
+// Epilogue of 4 consecutive columns n..n+3 of row m (vec: aligned vector
+// access allowed and all 4 columns < N).
+template <int EP>
+__device__ __forceinline__ void store_row4(const kr_gemm_args& g, int m, int n, kr_float4 acc,
+                                           bool vec) {
+    if (!vec) {
+        #pragma unroll
+        for (int r = 0; r < 4; r++)
+            if (n + r < g.N) store_one<EP>(g, m, n + r, acc[r]);
+        return;
+    }
+    const size_t o = (size_t)m * (size_t)g.ldo + (size_t)n;
+    if constexpr (EP == KR_EP_F32) {
+        *reinterpret_cast<kr_float4*>(reinterpret_cast<float*>(g.out) + o) = acc;
+    } else {
+        kr_half4 rv = kr_half4{0, 0, 0, 0}, gv = kr_half4{0, 0, 0, 0};
+        if constexpr (EP == KR_EP_RESID || EP == KR_EP_GATED) rv = *reinterpret_cast<const kr_half4*>(g.res + o);
+        if constexpr (EP == KR_EP_GATED) gv = *reinterpret_cast<const kr_half4*>(g.gate + o);
+        kr_half4 h;
+        #pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const float x = (float)kr_f16(acc[r]);
+            float y;
+            if constexpr (EP == KR_EP_F16) y = x;
+            else if constexpr (EP == KR_EP_SIGMOID) y = kr_sigmoid(x);
+            else if constexpr (EP == KR_EP_RELUSQ) { const float rr = x > 0.0f ? x : 0.0f; y = rr * rr; }
+            else if constexpr (EP == KR_EP_RESID) y = (float)rv[r] + x;
+            else y = (float)rv[r] + (float)kr_f16((float)gv[r] * x);
+            h[r] = kr_f16(y);
+        }
+        *reinterpret_cast<kr_half4*>(reinterpret_cast<kr_half*>(g.out) + o) = h;
+    }
+}
+
+// Tile t of the launch (same dealing as tile_of, for a launch of `grid`
+// virtual blocks): false past the last tile.
+__device__ __forceinline__ bool big_tile(const kr_gemm_args& g, int vb, int& m_t, int& n_t) {
+    const int gy = (g.M + kBigM - 1) / kBigM, gx = (g.N + kBigN - 1) / kBigN;
+    const int T = gx * gy, per = (T + 7) / 8;
+    const int t = (vb & 7) * per + (vb >> 3);
+    if (t >= T || (vb >> 3) >= per) return false;
+    const int in_group = kGroupM * gx;
+    const int first_m = (t / in_group) * kGroupM;
+    const int gm = min(gy - first_m, kGroupM);
+    const int r = t % in_group;
+    m_t = first_m + r % gm;
+    n_t = r / gm;
+    return true;
+}
+
+// Persistent: workgroup w takes virtual blocks w, w + G, w + 2G, ... (G =
+// gridDim.x, a multiple of 8, so a workgroup stays on one XCD) and keeps the
+// copy ring running across its tiles: the first two K steps of the next tile
+// are in flight while the current tile finishes and stores.
+template <int EP>
+__global__ void __launch_bounds__(512, 1) gemm_big_kernel(kr_gemm_args g, int n_virtual) {
+    __shared__ __attribute__((aligned(1024))) kr_half8 ring[3 * kBigStage];   // 3 x 48 KB
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave >> 1, wn = wave & 1;
+    const int G = gridDim.x;
+    const int KS = g.K / 64;                       // 64-wide K steps (K % 256 == 0)
+
+    // Copy instruction u = 6 wave + i of a stage: u < 32 fills A rows 8u..8u+7,
+    // u >= 32 fills W rows 8(u-32).. (rows past M or N repeat the last one;
+    // their outputs are never stored). Lane l moves chunk (row 8u' + l/8,
+    // kc = (l % 8) ^ ((row / 2) % 8)).
+    const unsigned ring_base = (unsigned)(uintptr_t)(__attribute__((address_space(3))) char*)ring;
+    unsigned dst[6];
+    int crow[6], ckc[6];
+    #pragma unroll
+    for (int i = 0; i < 6; i++) {
+        const int u = wave * 6 + i;
+        crow[i] = 8 * (u < 32 ? u : u - 32) + (lane >> 3);
+        ckc[i] = (lane & 7) ^ ((crow[i] >> 1) & 7);
+        dst[i] = ring_base + (unsigned)(u * 1024);
+    }
+    auto sources = [&](int m0, int n0, const char* (&src)[6]) {
+        #pragma unroll
+        for (int i = 0; i < 6; i++) {
+            if (wave * 6 + i < 32)
+                src[i] = reinterpret_cast<const char*>(g.A + (size_t)min(m0 + crow[i], g.M - 1) * g.lda + ckc[i] * 8);
+            else
+                src[i] = reinterpret_cast<const char*>(g.Wt + (size_t)min(n0 + crow[i], g.N - 1) * g.ldw + ckc[i] * 8);
+        }
+    };
+    // step number q of this workgroup (running over its tiles) -> ring stage q % 3
+    auto issue = [&](const char* (&src)[6], int ks, int q) {
+        const unsigned so = (unsigned)((q % 3) * kBigStage * 16);
+        #pragma unroll
+        for (int i = 0; i < 6; i++) big_copy(src[i] + (size_t)ks * 128, dst[i] + so);
+    };
+
+    int vb = blockIdx.x, m_t, n_t;
+    if (!big_tile(g, vb, m_t, n_t)) return;
+    const char* src[6];
+    const char* nsrc[6];
+    sources(m_t * kBigM, n_t * kBigN, src);
+    int q = 0;                                     // running step number
+    issue(src, 0, 0);
+    issue(src, 1, 1);
+    const int lr = lane & 15, lq = lane >> 4;
+    const uintptr_t ovec = EP == KR_EP_F32 ? 15 : 7;
+    const bool vec_ok = (g.ldo & 3) == 0 && ((uintptr_t)g.out & ovec) == 0 &&
+                        ((EP != KR_EP_RESID && EP != KR_EP_GATED) || ((uintptr_t)g.res & 7) == 0) &&
+                        (EP != KR_EP_GATED || ((uintptr_t)g.gate & 7) == 0);
+    while (true) {
+        const int m0 = m_t * kBigM, n0 = n_t * kBigN;
+        int nm_t = 0, nn_t = 0;
+        const bool has_next = vb + G < n_virtual && big_tile(g, vb + G, nm_t, nn_t);
+        if (has_next) sources(nm_t * kBigM, nn_t * kBigN, nsrc);
+        kr_float4 acc[4][4], tot[4][4];
+        for (int ks = 0; ks < KS; ks++, q++) {
+            // this wave's copies of step q have landed once at most the next
+            // step's remain in flight
+            const bool more = ks + 1 < KS || has_next;
+            if (more) asm volatile("s_waitcnt vmcnt(6)" ::: "memory");
+            else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            __syncthreads();   // every wave's copies of step q are in; step q-1's stage is free
+            if (ks + 2 < KS) issue(src, ks + 2, q + 2);
+            else if (has_next) issue(nsrc, ks + 2 - KS, q + 2);
+            const kr_half8* As = ring + (q % 3) * kBigStage;
+            const kr_half8* Ws = As + kBigM * 8;
+            if ((ks & 3) == 0) {
+                #pragma unroll
+                for (int i = 0; i < 4; i++)
+                    #pragma unroll
+                    for (int t = 0; t < 4; t++) acc[i][t] = kr_float4{0.f, 0.f, 0.f, 0.f};
+            }
+            #pragma unroll
+            for (int kb = 0; kb < 2; kb++) {
+                kr_half8 a[4], w[4];
+                #pragma unroll
+                for (int i = 0; i < 4; i++) a[i] = As[big_pos(64 * wm + 16 * i + lr, 4 * kb + lq)];
+                #pragma unroll
+                for (int t = 0; t < 4; t++) w[t] = Ws[big_pos(64 * wn + 16 * t + lr, 4 * kb + lq)];
+                #pragma unroll
+                for (int i = 0; i < 4; i++)
+                    #pragma unroll
+                    for (int t = 0; t < 4; t++)
+                        acc[i][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(w[t], a[i], acc[i][t], 0, 0, 0);
+            }
+            if ((ks & 3) == 3) {                   // end of a 256-wide K slice
+                #pragma unroll
+                for (int i = 0; i < 4; i++)
+                    #pragma unroll
+                    for (int t = 0; t < 4; t++) tot[i][t] = ks == 3 ? acc[i][t] : add4(tot[i][t], acc[i][t]);
+            }
+        }
+        // lane: row 64 wm + 16 i + lane % 16, columns 64 wn + 16 t + 4 (lane / 16) .. + 3
+        const bool full_m = m0 + kBigM <= g.M;
+        #pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int m = m0 + 64 * wm + 16 * i + lr;
+            if (!full_m && m >= g.M) continue;
+            #pragma unroll
+            for (int t = 0; t < 4; t++) {
+                const int n = n0 + 64 * wn + 16 * t + 4 * lq;
+                store_row4<EP>(g, m, n, tot[i][t], vec_ok && n + 3 < g.N);
+            }
+        }
+        if (!has_next) break;
+        vb += G;
+        m_t = nm_t;
+        n_t = nn_t;
+        #pragma unroll
+        for (int i = 0; i < 6; i++) src[i] = nsrc[i];
+    }
+}
+
+int launch_big(const kr_gemm_args& g, int ep, hipStream_t s) {
+    const long long T = (long long)((g.N + kBigN - 1) / kBigN) * ((g.M + kBigM - 1) / kBigM);
+    const int n_virtual = (int)((T + 7) / 8 * 8);
+    const int grid = n_virtual < 256 ? n_virtual : 256;   // one workgroup per CU
+    switch (ep) {
+        case KR_EP_F32: gemm_big_kernel<KR_EP_F32><<<grid, 512, 0, s>>>(g, n_virtual); break;
+        case KR_EP_F16: gemm_big_kernel<KR_EP_F16><<<grid, 512, 0, s>>>(g, n_virtual); break;
+        case KR_EP_SIGMOID: gemm_big_kernel<KR_EP_SIGMOID><<<grid, 512, 0, s>>>(g, n_virtual); break;
+        case KR_EP_RELUSQ: gemm_big_kernel<KR_EP_RELUSQ><<<grid, 512, 0, s>>>(g, n_virtual); break;
+        case KR_EP_RESID: gemm_big_kernel<KR_EP_RESID><<<grid, 512, 0, s>>>(g, n_virtual); break;
+        case KR_EP_GATED: gemm_big_kernel<KR_EP_GATED><<<grid, 512, 0, s>>>(g, n_virtual); break;
+        default: return kr_fail(KR_EINVAL, "unknown epilogue %d", ep);
+    }
+    KR_LAUNCHED();
+    return KR_OK;
+}
+
+// ---------------------------------------------------------------------------
 // Panel kernel (small M)
 // ---------------------------------------------------------------------------
 
@@ -629,6 +858,11 @@ int kr_gemm_launch_multi(const kr_gemm_args* jobs, const int* eps, int njobs, hi
         if (g.i8) {
             if (g.M >= 4096) rc = launch_tile<128, 128, true>(g, eps[j], s);
             else rc = launch_tile<64, 64, true>(g, eps[j], s);
+        } else if (g.M >= 4096 && g.K % 256 == 0 && (g.K >= 3072 || (g.N >= 3072 && g.N <= 16384))) {
+            // the channel-mix products; measured on MI355X the 768 x 768
+            // products (fp32 outputs) and the head run as fast or faster on
+            // the 128 x 128 kernel
+            rc = launch_big(g, eps[j], s);
         } else if (g.M >= 4096) {
             rc = launch_tile<128, 128, false>(g, eps[j], s);
         } else if (g.M > KR_GEMM_SMALL_M) {
