@@ -105,7 +105,13 @@ def gpu_bench(args, weights16, w8a8=False):
     x = torch.empty((M, P.C), dtype=torch.float16, device=dev)
     head_rows = min(M, 4096)
     logits = torch.empty((head_rows, P.V), dtype=torch.float16, device=dev)
-    pairs = torch.empty((M, 2), dtype=torch.int32, device=dev)
+    # the encoder of window w overlaps the forward of window w+1 (its own
+    # stream, double-buffered pairs), as in InferenceEngine.compress_tokens_batched
+    main = torch.cuda.current_stream(dev)
+    enc = torch.cuda.Stream(device=dev)
+    pairs = [torch.empty((M, 2), dtype=torch.int32, device=dev) for _ in range(2)]
+    fwd_done = [torch.cuda.Event() for _ in range(2)]
+    enc_done = [torch.cuda.Event() for _ in range(2)]
     cap = 4 * L + 64
     out = torch.zeros(B * cap, dtype=torch.uint8, device=dev)
     base = (torch.arange(B, dtype=torch.int32, device=dev) * cap).contiguous()
@@ -116,11 +122,18 @@ def gpu_bench(args, weights16, w8a8=False):
     cstate = State(P.n_layer, B, P.C, dev)
 
     def compress_window(w):
+        buf = pairs[w % 2]
+        if w >= 2:
+            main.wait_event(enc_done[w % 2])
         _lib.call("kr_compress_window", P.ptr, win_inp[w].data_ptr(), win_tok[w].data_ptr(), B, Tw,
                   cstate.ptr, x.data_ptr(), ws.data_ptr(), ws_bytes, logits.data_ptr(), P.V,
-                  head_rows, pairs.data_ptr(), PREC, s)
-        _lib.call("kr_encode_pairs_batched", pairs.data_ptr(), Tw, Tw, None, out.data_ptr(),
-                  out.numel(), base.data_ptr(), ac.data_ptr(), B, PREC, err.data_ptr(), s)
+                  head_rows, buf.data_ptr(), PREC, s)
+        fwd_done[w % 2].record(main)
+        enc.wait_event(fwd_done[w % 2])
+        _lib.call("kr_encode_pairs_batched", buf.data_ptr(), Tw, Tw, None, out.data_ptr(),
+                  out.numel(), base.data_ptr(), ac.data_ptr(), B, PREC, err.data_ptr(),
+                  enc.cuda_stream)
+        enc_done[w % 2].record(enc)
 
     for w in range(args.warmup):
         compress_window(w)
@@ -130,6 +143,7 @@ def gpu_bench(args, weights16, w8a8=False):
         compress_window(w)
     torch.cuda.synchronize()
     t_c = time.perf_counter() - t0
+    main.wait_stream(enc)
     _lib.call("kr_encode_finalize_batched", out.data_ptr(), out.numel(), base.data_ptr(),
               ac.data_ptr(), B, err.data_ptr(), s)
     torch.cuda.synchronize()
@@ -138,7 +152,7 @@ def gpu_bench(args, weights16, w8a8=False):
     comp_bytes = int(nbytes.sum().item())
 
     # ----------------------------------------------------------- decompress
-    del ws, x, logits, pairs
+    del ws, x, logits, pairs, enc
     G = max(1, min(args.groups, B))
     dws_bytes = _lib.lib().kr_decode_workspace_bytes(B, G, P.C, P.F)
     dws = torch.empty(dws_bytes, dtype=torch.uint8, device=dev)

@@ -142,20 +142,37 @@ class InferenceEngine:
         x = torch.empty((M, P.C), dtype=torch.float16, device=dev)
         head_rows = min(M, 2048)
         logits = torch.empty((head_rows, P.V), dtype=torch.float16, device=dev)
-        pairs = torch.empty((M, 2), dtype=torch.uint32, device=dev)
         lens_d = torch.from_numpy(lens.astype(np.int32)).to(dev)
         s = _lib.stream_ptr()
-        for w0 in range(0, Tmax, Tw):
+        # The range encoder (one lane per stream) of window w runs on its own
+        # stream while window w+1's forward runs: the (cdf[s], cdf[s+1]) pairs
+        # are double buffered, and the forward of window w+2 waits for the
+        # encoder of window w before overwriting its buffer.
+        main = torch.cuda.current_stream(dev)
+        enc = torch.cuda.Stream(device=dev)
+        pairs = [torch.empty((M, 2), dtype=torch.uint32, device=dev) for _ in range(2)]
+        fwd_done = [torch.cuda.Event() for _ in range(2)]
+        enc_done = [torch.cuda.Event() for _ in range(2)]
+        windows = list(range(0, Tmax, Tw))
+        n_valid = [(lens_d - w0).clamp(0, min(Tw, Tmax - w0)).to(torch.int32).contiguous()
+                   for w0 in windows]
+        for i, w0 in enumerate(windows):
             T = min(Tw, Tmax - w0)
             ids = inp_d[:, w0:w0 + T].contiguous()
             tgt = tok_d[:, w0:w0 + T].contiguous()
+            buf = pairs[i % 2]
+            if i >= 2:
+                main.wait_event(enc_done[i % 2])
             _lib.call("kr_compress_window", P.ptr, ids.data_ptr(), tgt.data_ptr(), B, T, state.ptr,
                       x.data_ptr(), ws.data_ptr(), nbytes, logits.data_ptr(), P.V, head_rows,
-                      pairs.data_ptr(), CDF_PRECISION, s)
-            n_valid = (lens_d - w0).clamp(0, T).to(torch.int32).contiguous()
-            _lib.call("kr_encode_pairs_batched", pairs.data_ptr(), T, T, n_valid.data_ptr(),
+                      buf.data_ptr(), CDF_PRECISION, s)
+            fwd_done[i % 2].record(main)
+            enc.wait_event(fwd_done[i % 2])
+            _lib.call("kr_encode_pairs_batched", buf.data_ptr(), T, T, n_valid[i].data_ptr(),
                       out.data_ptr(), out.numel(), base.data_ptr(), ac.data_ptr(), B,
-                      CDF_PRECISION, err.data_ptr(), s)
+                      CDF_PRECISION, err.data_ptr(), enc.cuda_stream)
+            enc_done[i % 2].record(enc)
+        main.wait_stream(enc)
         _lib.call("kr_encode_finalize_batched", out.data_ptr(), out.numel(), base.data_ptr(),
                   ac.data_ptr(), B, err.data_ptr(), s)
         if int(err.item()):
