@@ -104,7 +104,8 @@ def gpu_bench(args, weights16, w8a8=False):
     ws, ws_bytes = cpp_path.workspace(W, M)
     x = torch.empty((M, P.C), dtype=torch.float16, device=dev)
     head_rows = min(M, 4096)
-    logits = torch.empty((head_rows, P.V), dtype=torch.float16, device=dev)
+    ld = cpp_path.logits_ld(P.V)
+    logits = torch.empty((head_rows, ld), dtype=torch.float16, device=dev)
     # the encoder of window w overlaps the forward of window w+1 (its own
     # stream, double-buffered pairs), as in InferenceEngine.compress_tokens_batched
     main = torch.cuda.current_stream(dev)
@@ -126,7 +127,7 @@ def gpu_bench(args, weights16, w8a8=False):
         if w >= 2:
             main.wait_event(enc_done[w % 2])
         _lib.call("kr_compress_window", P.ptr, win_inp[w].data_ptr(), win_tok[w].data_ptr(), B, Tw,
-                  cstate.ptr, x.data_ptr(), ws.data_ptr(), ws_bytes, logits.data_ptr(), P.V,
+                  cstate.ptr, x.data_ptr(), ws.data_ptr(), ws_bytes, logits.data_ptr(), ld,
                   head_rows, buf.data_ptr(), PREC, s)
         fwd_done[w % 2].record(main)
         enc.wait_event(fwd_done[w % 2])
@@ -157,7 +158,7 @@ def gpu_bench(args, weights16, w8a8=False):
     dws_bytes = _lib.lib().kr_decode_workspace_bytes(B, G, P.C, P.F)
     dws = torch.empty(dws_bytes, dtype=torch.uint8, device=dev)
     dx = torch.empty((B, P.C), dtype=torch.float16, device=dev)
-    dlogits = torch.empty((B, P.V), dtype=torch.float16, device=dev)
+    dlogits = torch.empty((B, ld), dtype=torch.float16, device=dev)
     dac = torch.empty((B, 4), dtype=torch.uint32, device=dev)
     _lib.call("kr_decode_init_batched", out.data_ptr(), out.numel(), base.data_ptr(),
               nbytes.data_ptr(), dac.data_ptr(), B, s)
@@ -168,7 +169,7 @@ def gpu_bench(args, weights16, w8a8=False):
 
     def decode(n_steps):
         _lib.call("kr_decode_run", P.ptr, B, dstate.ptr, syms.data_ptr(), dx.data_ptr(),
-                  dws.data_ptr(), dws_bytes, dlogits.data_ptr(), P.V, out.data_ptr(), out.numel(),
+                  dws.data_ptr(), dws_bytes, dlogits.data_ptr(), ld, out.data_ptr(), out.numel(),
                   base.data_ptr(), nbytes.data_ptr(), dac.data_ptr(), dtoks.data_ptr(), L,
                   cnt.data_ptr(), None, PREC, n_steps, G, 1, s)
 

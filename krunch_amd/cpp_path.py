@@ -42,6 +42,12 @@ class Workspace:
 _WS: dict = {}
 
 
+
+def logits_ld(V: int) -> int:
+    """Row stride (elements) for engine-internal logits buffers: V rounded up
+    to a multiple of 8, so the head GEMM stores 8-byte vectors."""
+    return (int(V) + 7) // 8 * 8
+
 def workspace(weights, M: int):
     P: Prepared = weights["prepared"]
     nbytes = _lib.lib().kr_forward_workspace_bytes(M, P.C, P.F)

@@ -858,10 +858,10 @@ int kr_gemm_launch_multi(const kr_gemm_args* jobs, const int* eps, int njobs, hi
         if (g.i8) {
             if (g.M >= 4096) rc = launch_tile<128, 128, true>(g, eps[j], s);
             else rc = launch_tile<64, 64, true>(g, eps[j], s);
-        } else if (g.M >= 4096 && g.K % 256 == 0 && (g.K >= 3072 || (g.N >= 3072 && g.N <= 16384))) {
-            // the channel-mix products; measured on MI355X the 768 x 768
-            // products (fp32 outputs) and the head run as fast or faster on
-            // the 128 x 128 kernel
+        } else if (g.K % 256 == 0 && (g.M >= 4096 || (g.M >= 128 && g.N >= KR_GEMM_SMALL_MAX_N))) {
+            // large M, or the head at decode batch sizes: the persistent
+            // 256 x 128 kernel (vector epilogue when the output row stride is
+            // a multiple of 4 elements)
             rc = launch_big(g, eps[j], s);
         } else if (g.M >= 4096) {
             rc = launch_tile<128, 128, false>(g, eps[j], s);

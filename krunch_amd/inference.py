@@ -141,7 +141,8 @@ class InferenceEngine:
         ws, nbytes = cpp_path.workspace(W, M)
         x = torch.empty((M, P.C), dtype=torch.float16, device=dev)
         head_rows = min(M, 2048)
-        logits = torch.empty((head_rows, P.V), dtype=torch.float16, device=dev)
+        ld = cpp_path.logits_ld(P.V)
+        logits = torch.empty((head_rows, ld), dtype=torch.float16, device=dev)
         lens_d = torch.from_numpy(lens.astype(np.int32)).to(dev)
         s = _lib.stream_ptr()
         # The range encoder (one lane per stream) of window w runs on its own
@@ -164,7 +165,7 @@ class InferenceEngine:
             if i >= 2:
                 main.wait_event(enc_done[i % 2])
             _lib.call("kr_compress_window", P.ptr, ids.data_ptr(), tgt.data_ptr(), B, T, state.ptr,
-                      x.data_ptr(), ws.data_ptr(), nbytes, logits.data_ptr(), P.V, head_rows,
+                      x.data_ptr(), ws.data_ptr(), nbytes, logits.data_ptr(), ld, head_rows,
                       buf.data_ptr(), CDF_PRECISION, s)
             fwd_done[i % 2].record(main)
             enc.wait_event(fwd_done[i % 2])
@@ -221,9 +222,10 @@ class InferenceEngine:
         G = max(1, min(self.decode_groups, B))
         nbytes = _lib.lib().kr_decode_workspace_bytes(B, G, P.C, P.F)
         ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
-        logits = torch.empty((B, P.V), dtype=torch.float16, device=dev)
+        ld = cpp_path.logits_ld(P.V)
+        logits = torch.empty((B, ld), dtype=torch.float16, device=dev)
         _lib.call("kr_decode_run", P.ptr, B, state.ptr, syms.data_ptr(), x.data_ptr(),
-                  ws.data_ptr(), nbytes, logits.data_ptr(), P.V, inbuf.data_ptr(), inbuf.numel(),
+                  ws.data_ptr(), nbytes, logits.data_ptr(), ld, inbuf.data_ptr(), inbuf.numel(),
                   base.data_ptr(), limits.data_ptr(), ac.data_ptr(), tokens.data_ptr(), Tmax,
                   count.data_ptr(), ntd.data_ptr(), CDF_PRECISION, Tmax, G,
                   1 if self.use_graph else 0, s)
