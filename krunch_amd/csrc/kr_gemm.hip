@@ -307,14 +307,18 @@ __device__ __forceinline__ bool big_tile(const kr_gemm_args& g, int vb, int& m_t
 // gridDim.x, a multiple of 8, so a workgroup stays on one XCD) and keeps the
 // copy ring running across its tiles: the first two K steps of the next tile
 // are in flight while the current tile finishes and stores.
-template <int EP>
+// I8: int8 operands (w8a8), moved as 16-bit pairs: a 64-half K step is 128
+// int8 k and each 32-half block one v_mfma_i32_16x16x64_i8; the int32 sum is
+// exact (no slices), dequantised once per output: (float(acc) * sa[m]) * sw[n].
+template <int EP, bool I8>
 __global__ void __launch_bounds__(512, 1) gemm_big_kernel(kr_gemm_args g, int n_virtual) {
     __shared__ __attribute__((aligned(1024))) kr_half8 ring[3 * kBigStage];   // 3 x 48 KB
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave >> 1, wn = wave & 1;
     const int G = gridDim.x;
-    const int KS = g.K / 64;                       // 64-wide K steps (K % 256 == 0)
+    const int KS = (I8 ? g.K >> 1 : g.K) / 64;    // 64-half K steps (fp16: K % 256 == 0)
+    const long long lda16 = I8 ? g.lda >> 1 : g.lda, ldw16 = I8 ? g.ldw >> 1 : g.ldw;
 
     // Copy instruction u = 6 wave + i of a stage: u < 32 fills A rows 8u..8u+7,
     // u >= 32 fills W rows 8(u-32).. (rows past M or N repeat the last one;
@@ -334,9 +338,9 @@ __global__ void __launch_bounds__(512, 1) gemm_big_kernel(kr_gemm_args g, int n_
         #pragma unroll
         for (int i = 0; i < 6; i++) {
             if (wave * 6 + i < 32)
-                src[i] = reinterpret_cast<const char*>(g.A + (size_t)min(m0 + crow[i], g.M - 1) * g.lda + ckc[i] * 8);
+                src[i] = reinterpret_cast<const char*>(g.A + (size_t)min(m0 + crow[i], g.M - 1) * lda16 + ckc[i] * 8);
             else
-                src[i] = reinterpret_cast<const char*>(g.Wt + (size_t)min(n0 + crow[i], g.N - 1) * g.ldw + ckc[i] * 8);
+                src[i] = reinterpret_cast<const char*>(g.Wt + (size_t)min(n0 + crow[i], g.N - 1) * ldw16 + ckc[i] * 8);
         }
     };
     // step number q of this workgroup (running over its tiles) -> ring stage q % 3
@@ -364,7 +368,15 @@ __global__ void __launch_bounds__(512, 1) gemm_big_kernel(kr_gemm_args g, int n_
         int nm_t = 0, nn_t = 0;
         const bool has_next = vb + G < n_virtual && big_tile(g, vb + G, nm_t, nn_t);
         if (has_next) sources(nm_t * kBigM, nn_t * kBigN, nsrc);
-        kr_float4 acc[4][4], tot[4][4];
+        typedef typename std::conditional<I8, kr_int4, kr_float4>::type Acc;
+        Acc acc[4][4];
+        kr_float4 tot[4][4];
+        if constexpr (I8) {
+            #pragma unroll
+            for (int i = 0; i < 4; i++)
+                #pragma unroll
+                for (int t = 0; t < 4; t++) acc[i][t] = Acc{0, 0, 0, 0};
+        }
         for (int ks = 0; ks < KS; ks++, q++) {
             // this wave's copies of step q have landed once at most the next
             // step's remain in flight
@@ -376,11 +388,11 @@ __global__ void __launch_bounds__(512, 1) gemm_big_kernel(kr_gemm_args g, int n_
             else if (has_next) issue(nsrc, ks + 2 - KS, q + 2);
             const kr_half8* As = ring + (q % 3) * kBigStage;
             const kr_half8* Ws = As + kBigM * 8;
-            if ((ks & 3) == 0) {
+            if (!I8 && (ks & 3) == 0) {
                 #pragma unroll
                 for (int i = 0; i < 4; i++)
                     #pragma unroll
-                    for (int t = 0; t < 4; t++) acc[i][t] = kr_float4{0.f, 0.f, 0.f, 0.f};
+                    for (int t = 0; t < 4; t++) acc[i][t] = Acc{0, 0, 0, 0};
             }
             #pragma unroll
             for (int kb = 0; kb < 2; kb++) {
@@ -392,14 +404,34 @@ __global__ void __launch_bounds__(512, 1) gemm_big_kernel(kr_gemm_args g, int n_
                 #pragma unroll
                 for (int i = 0; i < 4; i++)
                     #pragma unroll
-                    for (int t = 0; t < 4; t++)
-                        acc[i][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(w[t], a[i], acc[i][t], 0, 0, 0);
+                    for (int t = 0; t < 4; t++) {
+                        if constexpr (I8)
+                            acc[i][t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(as_i4(w[t]), as_i4(a[i]),
+                                                                             acc[i][t], 0, 0, 0);
+                        else
+                            acc[i][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(w[t], a[i], acc[i][t], 0, 0, 0);
+                    }
             }
-            if ((ks & 3) == 3) {                   // end of a 256-wide K slice
-                #pragma unroll
-                for (int i = 0; i < 4; i++)
+            if constexpr (!I8) {
+                if ((ks & 3) == 3) {               // end of a 256-wide K slice
                     #pragma unroll
-                    for (int t = 0; t < 4; t++) tot[i][t] = ks == 3 ? acc[i][t] : add4(tot[i][t], acc[i][t]);
+                    for (int i = 0; i < 4; i++)
+                        #pragma unroll
+                        for (int t = 0; t < 4; t++) tot[i][t] = ks == 3 ? acc[i][t] : add4(tot[i][t], acc[i][t]);
+                }
+            }
+        }
+        if constexpr (I8) {   // dequantise: (float(acc) * sa[m]) * sw[n]
+            #pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const float sa = g.sa[min(m0 + 64 * wm + 16 * i + lr, g.M - 1)];
+                #pragma unroll
+                for (int t = 0; t < 4; t++) {
+                    const int n = n0 + 64 * wn + 16 * t + 4 * lq;
+                    #pragma unroll
+                    for (int r = 0; r < 4; r++)
+                        tot[i][t][r] = __fmul_rn(__fmul_rn((float)acc[i][t][r], sa), g.sw[min(n + r, g.N - 1)]);
+                }
             }
         }
         // lane: row 64 wm + 16 i + lane % 16, columns 64 wn + 16 t + 4 (lane / 16) .. + 3
@@ -423,17 +455,18 @@ __global__ void __launch_bounds__(512, 1) gemm_big_kernel(kr_gemm_args g, int n_
     }
 }
 
+template <bool I8>
 int launch_big(const kr_gemm_args& g, int ep, hipStream_t s) {
     const long long T = (long long)((g.N + kBigN - 1) / kBigN) * ((g.M + kBigM - 1) / kBigM);
     const int n_virtual = (int)((T + 7) / 8 * 8);
     const int grid = n_virtual < 256 ? n_virtual : 256;   // one workgroup per CU
     switch (ep) {
-        case KR_EP_F32: gemm_big_kernel<KR_EP_F32><<<grid, 512, 0, s>>>(g, n_virtual); break;
-        case KR_EP_F16: gemm_big_kernel<KR_EP_F16><<<grid, 512, 0, s>>>(g, n_virtual); break;
-        case KR_EP_SIGMOID: gemm_big_kernel<KR_EP_SIGMOID><<<grid, 512, 0, s>>>(g, n_virtual); break;
-        case KR_EP_RELUSQ: gemm_big_kernel<KR_EP_RELUSQ><<<grid, 512, 0, s>>>(g, n_virtual); break;
-        case KR_EP_RESID: gemm_big_kernel<KR_EP_RESID><<<grid, 512, 0, s>>>(g, n_virtual); break;
-        case KR_EP_GATED: gemm_big_kernel<KR_EP_GATED><<<grid, 512, 0, s>>>(g, n_virtual); break;
+        case KR_EP_F32: gemm_big_kernel<KR_EP_F32, I8><<<grid, 512, 0, s>>>(g, n_virtual); break;
+        case KR_EP_F16: gemm_big_kernel<KR_EP_F16, I8><<<grid, 512, 0, s>>>(g, n_virtual); break;
+        case KR_EP_SIGMOID: gemm_big_kernel<KR_EP_SIGMOID, I8><<<grid, 512, 0, s>>>(g, n_virtual); break;
+        case KR_EP_RELUSQ: gemm_big_kernel<KR_EP_RELUSQ, I8><<<grid, 512, 0, s>>>(g, n_virtual); break;
+        case KR_EP_RESID: gemm_big_kernel<KR_EP_RESID, I8><<<grid, 512, 0, s>>>(g, n_virtual); break;
+        case KR_EP_GATED: gemm_big_kernel<KR_EP_GATED, I8><<<grid, 512, 0, s>>>(g, n_virtual); break;
         default: return kr_fail(KR_EINVAL, "unknown epilogue %d", ep);
     }
     KR_LAUNCHED();
@@ -856,13 +889,14 @@ int kr_gemm_launch_multi(const kr_gemm_args* jobs, const int* eps, int njobs, hi
         KR_REQUIRE(g.Wt, "gemm: row-major W missing");
         int rc;
         if (g.i8) {
-            if (g.M >= 4096) rc = launch_tile<128, 128, true>(g, eps[j], s);
+            if (g.M >= 4096 && (g.K >> 1) % 64 == 0) rc = launch_big<true>(g, eps[j], s);
+            else if (g.M >= 4096) rc = launch_tile<128, 128, true>(g, eps[j], s);
             else rc = launch_tile<64, 64, true>(g, eps[j], s);
         } else if (g.K % 256 == 0 && (g.M >= 4096 || (g.M >= 128 && g.N >= KR_GEMM_SMALL_MAX_N))) {
             // large M, or the head at decode batch sizes: the persistent
             // 256 x 128 kernel (vector epilogue when the output row stride is
             // a multiple of 4 elements)
-            rc = launch_big(g, eps[j], s);
+            rc = launch_big<false>(g, eps[j], s);
         } else if (g.M >= 4096) {
             rc = launch_tile<128, 128, false>(g, eps[j], s);
         } else if (g.M > KR_GEMM_SMALL_M) {
