@@ -28,6 +28,7 @@
 
 #include "kr_math.h"
 #include "kr_rc_device.h"
+#include "kr_wave.h"
 
 namespace {
 
@@ -80,12 +81,10 @@ struct RowShared {
 };
 
 __device__ __forceinline__ float wave_max(float v) {
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
-    return v;
+    return kr_wave_reduce(v, [](float a, float b) { return fmaxf(a, b); });
 }
 __device__ __forceinline__ int wave_isum(int v) {
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
-    return v;
+    return kr_wave_reduce(v, [](int a, int b) { return a + b; });
 }
 // (value desc, index asc) total order: the first maximum wins.
 __device__ __forceinline__ bool better(float pv, int pi, float bv, int bi) {
@@ -145,9 +144,9 @@ __device__ float row_sum_numpy(float (&v)[kMaxIt][17], const int (&len)[kMaxIt],
         #pragma unroll
         for (int k = 1; k < 16; k++)
             if (k < nf) r = r + v[it][k];
-        r = r + __shfl_xor(r, 1);
-        r = r + __shfl_xor(r, 2);
-        r = r + __shfl_xor(r, 4);
+        r = r + kr_xor<1>(r);
+        r = r + kr_xor<2>(r);
+        r = r + kr_xor<4>(r);
         float res = len[it] >= 8 ? r : -0.0f;
         #pragma unroll
         for (int t = 0; t < 7; t++) {
@@ -325,20 +324,23 @@ row_cdf_kernel(const void* __restrict__ input, long long ld, int n_rows, PlanArg
             }
         }
         if constexpr (MODE == M_DECODE) {
-            lsum += __shfl_xor(lsum, 1);
-            lsum += __shfl_xor(lsum, 2);
-            lsum += __shfl_xor(lsum, 4);
+            lsum += kr_xor<1>(lsum);
+            lsum += kr_xor<2>(lsum);
+            lsum += kr_xor<4>(lsum);
             if (j == 0 && L < P.n_leaves) sh.leaf_count[L] = lsum;
         }
     }
 
     // ---- argmax (first maximum) and integer sums across the workgroup ----
-    for (int o = 32; o > 0; o >>= 1) {
-        const float ov = __shfl_xor(bp, o);
-        const int oi = __shfl_xor(bi, o);
-        const int oL = __shfl_xor(bL, o);
+    auto arg_step = [&](float ov, int oi, int oL) {
         if (better(ov, oi, bp, bi)) { bp = ov; bi = oi; bL = oL; }
-    }
+    };
+    arg_step(kr_xor<32>(bp), kr_xor<32>(bi), kr_xor<32>(bL));
+    arg_step(kr_xor<16>(bp), kr_xor<16>(bi), kr_xor<16>(bL));
+    arg_step(kr_xor<8>(bp), kr_xor<8>(bi), kr_xor<8>(bL));
+    arg_step(kr_xor<4>(bp), kr_xor<4>(bi), kr_xor<4>(bL));
+    arg_step(kr_xor<2>(bp), kr_xor<2>(bi), kr_xor<2>(bL));
+    arg_step(kr_xor<1>(bp), kr_xor<1>(bi), kr_xor<1>(bL));
     csum = wave_isum(csum);
     if constexpr (MODE == M_PAIRS) {
         cpre = wave_isum(cpre);

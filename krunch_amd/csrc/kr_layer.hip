@@ -17,6 +17,7 @@
 
 #include "kr_gemm.h"
 #include "kr_model.h"
+#include "kr_wave.h"
 
 namespace {
 
@@ -43,8 +44,7 @@ __device__ __forceinline__ void load_row(const kr_half* __restrict__ p, int lane
 }
 
 __device__ __forceinline__ float wave_sum(float s) {
-    for (int o = 32; o > 0; o >>= 1) s = s + __shfl_xor(s, o);
-    return s;
+    return kr_wave_reduce(s, [](float a, float b) { return a + b; });
 }
 
 // Per-lane copies of a [C] fp16 coefficient vector (the lane's 4-column groups).
@@ -146,7 +146,7 @@ __device__ __forceinline__ void store_mix_q8(int8_t* __restrict__ out, float* __
             v[i][q] = (float)kr_f16(cur.v[i][q] * m + prev.v[i][q] * (1.0f - m));
             amax = fmaxf(amax, fabsf(v[i][q]));
         }
-    for (int o = 32; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
+    amax = kr_wave_reduce(amax, [](float a, float b) { return fmaxf(a, b); });
     const float s = amax > 0.0f ? amax / 127.0f : 1.0f;
     #pragma unroll
     for (int i = 0; i < G; i++) {

@@ -9,11 +9,12 @@
 // The output is row-major [M, K] int8 or fragment-packed (kr_frag_index_i8),
 // the operand layout of the small-M int8 GEMM.
 #include "kr_gemm.h"
+#include "kr_wave.h"
 
 namespace {
 
 __device__ __forceinline__ float wave_maxf(float v) {
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+    v = kr_wave_reduce(v, [](float a, float b) { return fmaxf(a, b); });
     return v;
 }
 
