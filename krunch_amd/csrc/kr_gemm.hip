@@ -746,12 +746,14 @@ int launch_panel(kr_gemm_multi mj, hipStream_t s) {
     return KR_OK;
 }
 
-// Shapes compiled per block size: up to 12 slices TM {1, 2} x NS {1, 2};
-// up to 16 slices TM 1 x NS {1, 2}. Wider panels (NS > 2) cut the bytes a CU
-// reads but, with the registers a wave has, the third panel's loads wait for
-// the first panel's MFMAs: measured on MI355X at M = 256 they are 25-55%
-// slower, so every wave keeps all of its operand loads in flight at once.
-constexpr PanelShape kShapes256[] = {{1, 1}, {1, 2}, {2, 1}, {2, 2}};
+// Shapes compiled per block size: up to 4 slices TM {1, 2, 4} x NS {1, 2};
+// up to 12 slices TM {1, 2} x NS {1, 2}; up to 16 slices TM 1 x NS {1, 2}.
+// Wider panels (NS > 2) cut the bytes a CU reads but, with the registers a
+// wave has, the third panel's loads wait for the first panel's MFMAs:
+// measured on MI355X at M = 256 they are 25-55% slower, so every wave keeps
+// all of its operand loads in flight at once. Taller tiles (TM = 4) keep
+// that property at K <= 1024, where the A fragments of 4 row blocks fit.
+constexpr PanelShape kShapes256[] = {{1, 1}, {1, 2}, {2, 1}, {2, 2}, {4, 1}, {4, 2}};
 constexpr PanelShape kShapes768[] = {{1, 1}, {1, 2}, {2, 1}, {2, 2}};
 constexpr PanelShape kShapes1024[] = {{1, 1}, {1, 2}};
 
@@ -779,7 +781,9 @@ int launch_best(const kr_gemm_multi& mj, const PanelShape (&shapes)[N], hipStrea
     }
 #define KR_PANEL(TM_, NS_) \
     if (best.TM == TM_ && best.NS == NS_) return launch_panel<TM_, NS_, FRAG, MAXT, I8>(mj, s);
-    if constexpr (MAXT == 256 || MAXT == 768) {
+    if constexpr (MAXT == 256) {
+        KR_PANEL(1, 1) KR_PANEL(1, 2) KR_PANEL(2, 1) KR_PANEL(2, 2) KR_PANEL(4, 1) KR_PANEL(4, 2)
+    } else if constexpr (MAXT == 768) {
         KR_PANEL(1, 1) KR_PANEL(1, 2) KR_PANEL(2, 1) KR_PANEL(2, 2)
     } else {
         KR_PANEL(1, 1) KR_PANEL(1, 2)
