@@ -46,14 +46,16 @@ def parse():
     ap.add_argument("--no-w8a8", action="store_true",
                     help="skip the w8a8 codec (BASELINE config 4) run on the same windows")
     ap.add_argument("--kernel-probe", action="store_true",
-                    help="only run a 256 MiB device copy (counter calibration) and 8 launches of "
-                         "the dominant kernel, for rocprofv3 --pmc runs")
+                    help="only run a 256 MiB device copy (counter calibration), 8 launches of "
+                         "the dominant kernel and 2 eager launches of each other hot kernel at "
+                         "the bench shapes, for rocprofv3 --pmc runs")
     return ap.parse_args()
 
 
 def kernel_probe(weights16, B):
     """A plain copy of known size, then the dominant kernel, eagerly (one
     dispatch each), so hardware counters can be read per dispatch."""
+    import ctypes
     import torch
     from krunch_amd import _lib, cpp_path
 
@@ -74,6 +76,58 @@ def kernel_probe(weights16, B):
     for _ in range(8):
         _lib.call("kr_det_matmul_packed", Af.data_ptr(), M, K, Wf.data_ptr(), N, out.data_ptr(), N,
                   5, res.data_ptr(), gate.data_ptr(), 0, _lib.stream_ptr())
+    torch.cuda.synchronize()
+    del A, Af, res, gate, out
+    s = _lib.stream_ptr()
+    # one stepped layer (LN-mix, K/V/R+WKV, output projection, LN-mix, ffn R/K, ffn V) at B rows
+    from krunch_amd.model import State
+    st = State(P.n_layer, B, P.C, dev)
+    ws, nbytes = cpp_path.workspace(W, B)
+    x = torch.randn((B, P.C), device=dev).half()
+    L0 = P.layers_c[0]
+    att_xx, aa0, bb0, pp0, ffn_xx = st._layer(0)
+    for _ in range(2):
+        _lib.call("kr_layer_step", ctypes.byref(L0), P.C, P.F, x.data_ptr(), B, 1,
+                  att_xx.data_ptr(), aa0.data_ptr(), bb0.data_ptr(), pp0.data_ptr(),
+                  ffn_xx.data_ptr(), ws.data_ptr(), nbytes, s)
+    torch.cuda.synchronize()
+    del ws
+    # packed channel-mix value product at the window shape (B * 1024 rows) on the large-M kernel
+    Mp = B * 1024
+    A = torch.rand((Mp, K), device=dev).half()
+    res = torch.randn((Mp, N), device=dev).half()
+    gate = torch.rand((Mp, N), device=dev).half()
+    out = torch.empty((Mp, N), dtype=torch.float16, device=dev)
+    Wt = P.tensors["0.fVt"]
+    for _ in range(2):
+        _lib.call("kr_det_matmul", A.data_ptr(), Mp, K, Wt.data_ptr(), K, N, out.data_ptr(), N, 5,
+                  res.data_ptr(), gate.data_ptr(), s)
+    torch.cuda.synchronize()
+    del A, res, gate, out
+    # packed WKV over a 1024-token window of B streams
+    k = torch.randn((B, 1024, P.C), device=dev)
+    v = torch.randn((B, 1024, P.C), device=dev)
+    r = torch.rand((B, 1024, P.C), device=dev).half()
+    ry = torch.empty_like(r)
+    aa = torch.zeros((B, P.C), device=dev)
+    bb = torch.zeros((B, P.C), device=dev)
+    pp = torch.full((B, P.C), -1e30, device=dev)
+    dec = P.tensors["0.decay"]
+    fst = P.tensors["0.first"]
+    for _ in range(2):
+        _lib.call("kr_wkv", B, 1024, P.C, dec.data_ptr(), fst.data_ptr(), k.data_ptr(), v.data_ptr(),
+                  r.data_ptr(), aa.data_ptr(), bb.data_ptr(), pp.data_ptr(), ry.data_ptr(), s)
+    torch.cuda.synchronize()
+    del k, v, r, ry
+    # softmax -> CDF -> symbol interval for 4096 rows of logits (the compress CDF stage)
+    rows = 4096
+    ld = cpp_path.logits_ld(P.V)
+    logits = (torch.randn((rows, ld), device=dev) * 3).half()
+    syms = torch.randint(0, P.V, (rows,), device=dev, dtype=torch.int32)
+    pairs = torch.empty((rows, 2), dtype=torch.int32, device=dev)
+    for _ in range(2):
+        _lib.call("kr_softmax_cdf_pairs", logits.data_ptr(), rows, P.V, ld, syms.data_ptr(),
+                  pairs.data_ptr(), 24, s)
     torch.cuda.synchronize()
     print(json.dumps({"probe": "ok", "copy_bytes": 2 * src.numel() * 4}))
 
