@@ -91,31 +91,43 @@ __device__ __forceinline__ bool better(float pv, int pi, float bv, int bi) {
     return pv > bv || (pv == bv && pi < bi);
 }
 
-// fp16 logits rows are first copied into LDS with 16-byte loads (element i
-// at stage[i + pad], pad making the copied chunks 16-byte aligned), then read
-// in the scattered leaf layout from there: the leaf layout read straight from
-// global memory requests every cache line about ten times.
-constexpr int kStageMax = 65536 + 16;
+// fp16 logits rows are first copied into LDS with 16-byte loads, then read in
+// the scattered leaf layout from there: the leaf layout read straight from
+// global memory requests every cache line about ten times. Element i sits at
+// stage[pad + i + skew(i)]: pad makes the copied 16-byte chunks aligned, and
+// skew adds 8 halves (16 bytes, 4 banks) per 128 elements past the unaligned
+// head. Inside a full 8192-element block every leaf is 128 elements long, so
+// without the skew the 8 leaves one gather instruction reads (8 lanes each)
+// start 256 bytes apart, on the same 4 banks: an 8-way bank conflict.
+constexpr int kStageMax = 65536 + 8 * (65536 / 128) + 16;
+
+struct StageMap {
+    int pad, head;
+    __device__ __forceinline__ int at(int i) const {
+        return pad + i + (i >= head ? ((i - head) >> 7) << 3 : 0);
+    }
+};
 
 template <int IN>
-__device__ __forceinline__ float load_val(const void* row, const kr_half* stage, int pad, int i) {
-    if constexpr (IN == IN_LOGITS_F16) return (float)stage[pad + i];
+__device__ __forceinline__ float load_val(const void* row, const kr_half* stage, StageMap sm, int i) {
+    if constexpr (IN == IN_LOGITS_F16) return (float)stage[sm.at(i)];
     else return reinterpret_cast<const float*>(row)[i];
 }
 
-// Copy V fp16 values at rp (2-byte aligned) into stage[pad ..], pad in [0, 8).
-__device__ __forceinline__ int stage_row(const kr_half* __restrict__ rp, int V, kr_half* stage,
-                                         int tid) {
+// Copy V fp16 values at rp (2-byte aligned) into the stage (see StageMap).
+__device__ __forceinline__ StageMap stage_row(const kr_half* __restrict__ rp, int V, kr_half* stage,
+                                              int tid) {
     const int head = min((int)(((16 - ((uintptr_t)rp & 15)) & 15) >> 1), V);
     const int pad = (8 - head) & 7;
+    const StageMap sm{pad, head};
     const int nchunks = (V - head) / 8;
     for (int c = tid; c < nchunks; c += kThreads)
-        *reinterpret_cast<kr_half8*>(stage + pad + head + 8 * c) =
+        *reinterpret_cast<kr_half8*>(stage + pad + head + 8 * c + ((c >> 4) << 3)) =
             *reinterpret_cast<const kr_half8*>(rp + head + 8 * c);
     const int tail0 = head + 8 * nchunks;
-    if (tid < head) stage[pad + tid] = rp[tid];
-    if (tid >= 8 && tid - 8 < V - tail0) stage[pad + tail0 + tid - 8] = rp[tail0 + tid - 8];
-    return pad;
+    if (tid < head) stage[sm.at(tid)] = rp[tid];
+    if (tid >= 8 && tid - 8 < V - tail0) stage[sm.at(tail0 + tid - 8)] = rp[tail0 + tid - 8];
+    return sm;
 }
 
 // a / b correctly rounded (IEEE binary32, round to nearest), given
@@ -209,7 +221,7 @@ row_cdf_kernel(const void* __restrict__ input, long long ld, int n_rows, PlanArg
     else
         rowp = reinterpret_cast<const char*>(input) + (size_t)row * (size_t)ld * 4;
 
-    int pad = 0;
+    StageMap pad{0, 0};
     if constexpr (IN == IN_LOGITS_F16) {
         pad = stage_row(reinterpret_cast<const kr_half*>(rowp), V, stage, tid);
         if constexpr (MODE == M_DECODE) {
@@ -234,6 +246,18 @@ row_cdf_kernel(const void* __restrict__ input, long long ld, int n_rows, PlanArg
         start[it] = lf.x;
         len[it] = lf.y;
         const int nf = leaf_full(lf.y), rm = leaf_rem(lf.y);
+        if constexpr (IN == IN_LOGITS_F16) {
+            // a leaf inside one 128-element skew segment (every leaf of a
+            // full 8192-element block) reads at one constant offset
+            const int s0 = pad.at(lf.x) - lf.x;
+            if (lf.y == 0 || pad.at(lf.x + lf.y - 1) - (lf.x + lf.y - 1) == s0) {
+                const kr_half* sp = stage + lf.x + s0;
+                #pragma unroll
+                for (int k = 0; k < 16; k++) v[it][k] = k < nf ? (float)sp[j + 8 * k] : -INFINITY;
+                v[it][16] = j < rm ? (float)sp[8 * nf + j] : -INFINITY;
+                continue;
+            }
+        }
         #pragma unroll
         for (int k = 0; k < 16; k++)
             v[it][k] = k < nf ? load_val<IN>(rowp, stage, pad, lf.x + j + 8 * k) : -INFINITY;
