@@ -38,6 +38,8 @@ constexpr int kLeavesPerIt = kWaves * 8;     // 128 leaves per register slice
 constexpr int kMaxIt = 4;                    // up to 512 leaves: V <= 65536
 constexpr int kMaxLeaves = kMaxIt * kLeavesPerIt;
 constexpr int kMaxNodes = 2 * kMaxLeaves;
+constexpr int kMaxLevels = 16;               // tree height above the leaves
+constexpr int kMaxBlocks = 8;                // 8192-element blocks: V <= 65536
 
 enum : int { IN_LOGITS_F16 = 0, IN_PROBS_F32 = 1 };
 enum : int { M_CDF = 0, M_COUNTS = 1, M_PROBS = 2, M_PAIRS = 3, M_DECODE = 4 };
@@ -65,6 +67,9 @@ struct DecodeArgs {
 
 struct RowShared {
     float node[kMaxNodes];
+    int2 inner[kMaxLeaves];                  // the summation plan, copied once
+    int level_start[kMaxLevels + 1];
+    int roots[kMaxBlocks];
     int leaf_count[kMaxLeaves];
     int leaf_buf[128];
     float redf[kWaves];
@@ -99,7 +104,9 @@ __device__ __forceinline__ bool better(float pv, int pi, float bv, int bi) {
 // head. Inside a full 8192-element block every leaf is 128 elements long, so
 // without the skew the 8 leaves one gather instruction reads (8 lanes each)
 // start 256 bytes apart, on the same 4 banks: an 8-way bank conflict.
-constexpr int kStageMax = 65536 + 8 * (65536 / 128) + 16;
+// The last 136 halves are room for the gather's reads past the end of a leaf
+// (up to 135 halves past a leaf's first staged element), discarded after.
+constexpr int kStageMax = 65536 + 8 * (65536 / 128) + 16 + 136;
 
 struct StageMap {
     int pad, head;
@@ -141,59 +148,122 @@ __device__ __forceinline__ float div_by(float a, float b, float y) {
     return __builtin_fmaf(__builtin_fmaf(-q, b, a), y, q);
 }
 
-// Sum of all held values in numpy's order (see file header). Every thread
-// returns the same value.
 __device__ __forceinline__ int leaf_full(int len) { return len >= 8 ? (len >> 3) : 0; }
 __device__ __forceinline__ int leaf_rem(int len) { return len >= 8 ? (len & 7) : len; }
 
-__device__ float row_sum_numpy(float (&v)[kMaxIt][17], const int (&len)[kMaxIt],
+// The value of v in lane (lane + T) of the same 16-lane row (DPP row_shl:T).
+// Read only by lanes at offset 0 or 8 of a row with T <= 7, whose source
+// lanes lie inside the row.
+template <int T>
+__device__ __forceinline__ float row_shl(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v),
+                                                                 0x100 + T, 0xF, 0xF, false));
+}
+
+// Sum of all held values in numpy's order (see file header). Every thread
+// returns the same value. Slots that hold no element of the row carry +0.0
+// and are added unconditionally: x + 0.0 == x for every x except -0.0, and
+// a signed zero can only decide the sign of a partial sum that is exactly
+// zero, which then adds exactly into any nonzero sum, so only an all-zero
+// row can differ (in the sign of its zero total).
+__device__ float row_sum_numpy(const float (&v)[kMaxIt][17], const int (&len)[kMaxIt],
                                const PlanArgs& P, RowShared& sh, int lane, int wave) {
     const int grp = lane >> 3, j = lane & 7;
     #pragma unroll
     for (int it = 0; it < kMaxIt; it++) {
-        const int nf = leaf_full(len[it]), rm = leaf_rem(len[it]);
         float r = v[it][0];
         #pragma unroll
-        for (int k = 1; k < 16; k++)
-            if (k < nf) r = r + v[it][k];
+        for (int k = 1; k < 16; k++) r = r + v[it][k];
         r = r + kr_xor<1>(r);
         r = r + kr_xor<2>(r);
         r = r + kr_xor<4>(r);
+        // the len % 8 tail elements, in order, onto lane 0 of the group
+        const float t = v[it][16];
         float res = len[it] >= 8 ? r : -0.0f;
-        #pragma unroll
-        for (int t = 0; t < 7; t++) {
-            const float tv = __shfl(v[it][16], (grp << 3) + t);
-            if (t < rm) res = res + tv;
-        }
+        res = res + t;
+        res = res + row_shl<1>(t);
+        res = res + row_shl<2>(t);
+        res = res + row_shl<3>(t);
+        res = res + row_shl<4>(t);
+        res = res + row_shl<5>(t);
+        res = res + row_shl<6>(t);
         const int L = it * kLeavesPerIt + wave * 8 + grp;
         if (j == 0 && L < P.n_leaves) sh.node[L] = res;
     }
     __syncthreads();
-    for (int lev = 0; lev < P.n_levels; lev++) {
-        const int s = P.level_start[lev], e = P.level_start[lev + 1];
-        for (int idx = s + (int)threadIdx.x; idx < e; idx += kThreads) {
-            const int2 ch = P.inner[idx];
-            sh.node[P.n_leaves + idx] = sh.node[ch.x] + sh.node[ch.y];
+    // Inner nodes level by level, then the blocks left to right, by wave 0
+    // alone: a wave's LDS accesses execute in program order, so each level
+    // reads the previous one's writes without a workgroup barrier.
+    if (wave == 0) {
+        for (int lev = 0; lev < P.n_levels; lev++) {
+            const int s = sh.level_start[lev], e = sh.level_start[lev + 1];
+            for (int idx = s + lane; idx < e; idx += 64) {
+                const int2 ch = sh.inner[idx];
+                sh.node[P.n_leaves + idx] = sh.node[ch.x] + sh.node[ch.y];
+            }
+            __builtin_amdgcn_wave_barrier();
         }
-        __syncthreads();
-    }
-    if (threadIdx.x == 0) {
-        float acc = 0.0f;
-        for (int b = 0; b < P.n_blocks; b++) acc = acc + sh.node[P.roots[b]];
-        sh.total = acc;
+        if (lane == 0) {
+            float acc = 0.0f;
+            for (int b = 0; b < P.n_blocks; b++) acc = acc + sh.node[sh.roots[b]];
+            sh.total = acc;
+        }
     }
     __syncthreads();
     return sh.total;
 }
 
+// Element index of slot k (0..16) of a leaf (start, len) held by lane j.
+__device__ __forceinline__ int slot_index(int start, int len, int j, int k) {
+    return k < 16 ? start + j + 8 * k : start + 8 * leaf_full(len) + j;
+}
+
+// floor(p * scale) as an int. From logits p >= 0 (or NaN), and truncation is
+// the floor there: one conversion instead of a floor and a conversion.
+template <int IN>
+__device__ __forceinline__ int scaled_floor(float p, float scale) {
+    if constexpr (IN == IN_LOGITS_F16) return (int)__fmul_rn(p, scale);
+    else return (int)floorf(__fmul_rn(p, scale));
+}
+
+// 16-byte asynchronous copy global -> LDS: lane l writes LDS byte address
+// lds + 16 l. The compiler does not count it: readers wait with an explicit
+// s_waitcnt vmcnt(0) and a barrier.
+__device__ __forceinline__ void lds_copy16(const void* src, unsigned lds) {
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off"
+                 :: "s"(lds), "v"(src) : "memory", "m0");
+}
+
+// stage_row's layout for a 16-byte-aligned row whose last chunk of 8 lies
+// inside its allocation (row stride a multiple of 8): chunk c at 16-byte unit
+// c + c / 16, so unit 17 s + t holds chunk 16 s + t for t < 16 and unit
+// 17 s + 16 is the skew gap. Each wave copy fills 64 consecutive units; a gap
+// lane re-reads its neighbour's chunk (same cache line) and lanes past the
+// row re-read the last chunk. Values past V (the row's padding) are never
+// gathered as elements. The copies are left in flight.
+__device__ __forceinline__ void stage_row_async(const kr_half* rp, int V, unsigned stage_lds,
+                                                int lane, int wave) {
+    const int nch = (V + 7) >> 3;
+    const int last = nch - 1 + ((nch - 1) >> 4);           // unit of the last chunk
+    // q is wave-uniform (the LDS base goes through an SGPR into M0)
+    for (int q = __builtin_amdgcn_readfirstlane(wave); 64 * q <= last; q += kWaves) {
+        const int u = 64 * q + lane;
+        const int s = (u * 61681) >> 20;                    // u / 17 for u < 20000
+        const int c = min(16 * s + min(u - 17 * s, 15), nch - 1);
+        lds_copy16(rp + 8 * c, stage_lds + 1024u * (unsigned)q);
+    }
+}
+
+// One row of the CDF stage. async_stage: the row is already being copied
+// into the stage (stage_row_async) and, once it is gathered, the copy of
+// next_row (>= 0) is started, to land while this row is computed.
 template <int IN, int MODE>
-__global__ void __launch_bounds__(kThreads)
-row_cdf_kernel(const void* __restrict__ input, long long ld, int n_rows, PlanArgs P, int prec,
-               void* __restrict__ out, long long out_ld, const int32_t* __restrict__ symbols,
-               DecodeArgs D) {
-    __shared__ RowShared sh;
-    __shared__ __attribute__((aligned(16))) kr_half stage[IN == IN_LOGITS_F16 ? kStageMax : 8];
-    const int row = blockIdx.x;
+__device__ __forceinline__ void cdf_row(const void* __restrict__ input, long long ld, int row,
+                                        int next_row, const PlanArgs& P, int prec,
+                                        void* __restrict__ out, long long out_ld,
+                                        const int32_t* __restrict__ symbols, const DecodeArgs& D,
+                                        RowShared& sh, kr_half* stage, unsigned stage_lds,
+                                        bool async_stage) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int grp = lane >> 3, j = lane & 7;
     const int V = P.V;
@@ -223,7 +293,8 @@ row_cdf_kernel(const void* __restrict__ input, long long ld, int n_rows, PlanArg
 
     StageMap pad{0, 0};
     if constexpr (IN == IN_LOGITS_F16) {
-        pad = stage_row(reinterpret_cast<const kr_half*>(rowp), V, stage, tid);
+        if (async_stage) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        else pad = stage_row(reinterpret_cast<const kr_half*>(rowp), V, stage, tid);
         if constexpr (MODE == M_DECODE) {
             if (tid == 0) {   // parked in LDS until the symbol is known
                 sh.dstate = dst;
@@ -235,7 +306,8 @@ row_cdf_kernel(const void* __restrict__ input, long long ld, int n_rows, PlanArg
         __syncthreads();
     }
 
-    // ---- gather the row into registers, leaf layout ----
+    // ---- gather the row into registers, leaf layout; slots that hold no
+    // element get -inf (softmax input, and the argmax of probabilities) ----
     float v[kMaxIt][17];
     int start[kMaxIt], len[kMaxIt];
     #pragma unroll
@@ -247,14 +319,26 @@ row_cdf_kernel(const void* __restrict__ input, long long ld, int n_rows, PlanArg
         len[it] = lf.y;
         const int nf = leaf_full(lf.y), rm = leaf_rem(lf.y);
         if constexpr (IN == IN_LOGITS_F16) {
-            // a leaf inside one 128-element skew segment (every leaf of a
-            // full 8192-element block) reads at one constant offset
+            // A leaf inside one 128-element skew segment (every leaf of a
+            // full 8192-element block) reads at one constant offset. Slots
+            // past the leaf read other staged values (the stage has room
+            // for them) that the select then discards.
             const int s0 = pad.at(lf.x) - lf.x;
             if (lf.y == 0 || pad.at(lf.x + lf.y - 1) - (lf.x + lf.y - 1) == s0) {
                 const kr_half* sp = stage + lf.x + s0;
+                if (lf.y == 128) {   // a full leaf: 16 slots of 8, no tail
+                    #pragma unroll
+                    for (int k = 0; k < 16; k++) v[it][k] = (float)sp[j + 8 * k];
+                    v[it][16] = -INFINITY;
+                    continue;
+                }
                 #pragma unroll
-                for (int k = 0; k < 16; k++) v[it][k] = k < nf ? (float)sp[j + 8 * k] : -INFINITY;
-                v[it][16] = j < rm ? (float)sp[8 * nf + j] : -INFINITY;
+                for (int k = 0; k < 16; k++) {
+                    const float x = (float)sp[j + 8 * k];
+                    v[it][k] = k < nf ? x : -INFINITY;
+                }
+                const float x = (float)sp[8 * nf + j];
+                v[it][16] = j < rm ? x : -INFINITY;
                 continue;
             }
         }
@@ -264,20 +348,27 @@ row_cdf_kernel(const void* __restrict__ input, long long ld, int n_rows, PlanArg
         v[it][16] = j < rm ? load_val<IN>(rowp, stage, pad, lf.x + 8 * nf + j) : -INFINITY;
     }
 
-    float inv_S = 1.0f;
+    // ---- row max (exact, order-free): of the logits, or of the probabilities ----
     float m = -INFINITY;
+    #pragma unroll
+    for (int it = 0; it < kMaxIt; it++)
+        #pragma unroll
+        for (int k = 0; k < 17; k++) m = fmaxf(m, v[it][k]);
+    m = wave_max(m);
+    if (lane == 0) sh.redf[wave] = m;
+    __syncthreads();
+    // every wave has gathered: the stage is free for the next row
+    if (IN == IN_LOGITS_F16 && async_stage && next_row >= 0)
+        stage_row_async(reinterpret_cast<const kr_half*>(input) + (size_t)next_row * (size_t)ld, V,
+                        stage_lds, lane, wave);
+    m = sh.redf[0];
+    #pragma unroll
+    for (int w = 1; w < kWaves; w++) m = fmaxf(m, sh.redf[w]);
+
+    // qmax: the largest value the CDF stage divides; p = q / denom is
+    // nondecreasing in q, so the largest p is qmax / denom.
+    float inv_S = 1.0f, qmax;
     if constexpr (IN == IN_LOGITS_F16) {
-        // ---- row max (exact, order-free) ----
-        #pragma unroll
-        for (int it = 0; it < kMaxIt; it++)
-            #pragma unroll
-            for (int k = 0; k < 17; k++) m = fmaxf(m, v[it][k]);
-        m = wave_max(m);
-        if (lane == 0) sh.redf[wave] = m;
-        __syncthreads();
-        m = sh.redf[0];
-        #pragma unroll
-        for (int w = 1; w < kWaves; w++) m = fmaxf(m, sh.redf[w]);
         // ---- e = kexp(x - m); S = numpy-order sum; q = e * (1/S) ----
         #pragma unroll
         for (int it = 0; it < kMaxIt; it++)
@@ -289,7 +380,10 @@ row_cdf_kernel(const void* __restrict__ input, long long ld, int n_rows, PlanArg
         for (int it = 0; it < kMaxIt; it++)
             #pragma unroll
             for (int k = 0; k < 17; k++) v[it][k] = __fmul_rn(v[it][k], inv_S);
+        // every e <= kexp(0) = 1, reached at the maximum logit
+        qmax = inv_S;
     } else {
+        qmax = m;
         #pragma unroll
         for (int it = 0; it < kMaxIt; it++)
             #pragma unroll
@@ -314,81 +408,104 @@ row_cdf_kernel(const void* __restrict__ input, long long ld, int n_rows, PlanArg
     const float denom = fmaxf(P_sum, 1e-30f);
     const float rdenom = 1.0f / denom;
     const float scale = (float)((1 << prec) - V);
+    const float pmax = div_by(qmax, denom, rdenom);
 
-    int sym = -1;
-    if constexpr (MODE == M_PAIRS) sym = symbols[row];
-
-    float bp = -1.0f;
-    int bi = 0x7fffffff, bL = 0;
-    int csum = 0, cpre = 0, csym = 0;
+    // ---- c = floor(p * scale) + 1 per element. Per leaf slice a lane keeps
+    // the sum of floor(p * scale) over its slots (an empty slot holds q = 0,
+    // so it adds 0) and adds its element count afterwards. The first maximum
+    // of p is the lowest index with p == pmax: slots are visited from the
+    // highest index down and the last hit is kept. With logits pmax > 0, so
+    // an empty slot (p = 0) never hits; probabilities check occupancy. ----
+    int lsum[kMaxIt];
+    int bslot = -1;                       // 32 * it + k of the first maximum held
     int32_t* orow = nullptr;
     if constexpr (MODE == M_CDF || MODE == M_COUNTS)
         orow = reinterpret_cast<int32_t*>(out) + (size_t)row * (size_t)out_ld;
+    #pragma unroll
+    for (int it = kMaxIt - 1; it >= 0; it--) {
+        const int nf = leaf_full(len[it]), rm = leaf_rem(len[it]);
+        int ls = 0;
+        #pragma unroll
+        for (int k = 16; k >= 0; k--) {
+            const float p = div_by(v[it][k], denom, rdenom);
+            const int f = scaled_floor<IN>(p, scale);
+            ls += f;
+            bool hit = p == pmax;
+            if constexpr (IN == IN_PROBS_F32 || MODE == M_CDF || MODE == M_COUNTS) {
+                const bool live = k < 16 ? (k < nf) : (j < rm);
+                if constexpr (IN == IN_PROBS_F32) hit = hit && live;
+                if constexpr (MODE == M_CDF || MODE == M_COUNTS)
+                    if (live) orow[slot_index(start[it], len[it], j, k) + 1] = f + 1;
+            }
+            if (hit) bslot = 32 * it + k;
+        }
+        lsum[it] = ls + nf + (j < rm ? 1 : 0);
+    }
+    int key = 0x7fffffff;                 // (index << 9) | leaf of that maximum
+    if (bslot >= 0) {
+        const int bi = bslot >> 5, bk = bslot & 31;
+        int st = start[0], ln = len[0];
+        #pragma unroll
+        for (int it = 1; it < kMaxIt; it++)
+            if (bi == it) { st = start[it]; ln = len[it]; }
+        key = (slot_index(st, ln, j, bk) << 9) | (bi * kLeavesPerIt + wave * 8 + grp);
+    }
 
+    int csum = 0, cpre = 0, csym = 0;
+    int sym = -1;
+    if constexpr (MODE == M_PAIRS) sym = symbols[row];
     #pragma unroll
     for (int it = 0; it < kMaxIt; it++) {
-        const int L = it * kLeavesPerIt + wave * 8 + grp;
-        const int nf = leaf_full(len[it]), rm = leaf_rem(len[it]);
-        int lsum = 0;
-        #pragma unroll
-        for (int k = 0; k < 17; k++) {
-            const bool live = k < 16 ? (k < nf) : (j < rm);
-            const int idx = k < 16 ? start[it] + j + 8 * k : start[it] + 8 * nf + j;
-            const float p = div_by(v[it][k], denom, rdenom);
-            const int c = (int)floorf(__fmul_rn(p, scale)) + 1;
-            if (live) {
-                if (better(p, idx, bp, bi)) { bp = p; bi = idx; bL = L; }
-                csum += c;
-                lsum += c;
-                if constexpr (MODE == M_CDF || MODE == M_COUNTS) orow[idx + 1] = c;
-                if constexpr (MODE == M_PAIRS) {
-                    if (idx < sym) cpre += c;
-                    if (idx == sym) csym = c;
+        csum += lsum[it];
+        if constexpr (MODE == M_PAIRS) {
+            if (start[it] + len[it] <= sym) {
+                cpre += lsum[it];
+            } else if (start[it] <= sym) {   // the leaf that holds the symbol
+                const int nf = leaf_full(len[it]), rm = leaf_rem(len[it]);
+                #pragma unroll
+                for (int k = 0; k < 17; k++) {
+                    const bool live = k < 16 ? (k < nf) : (j < rm);
+                    const int idx = slot_index(start[it], len[it], j, k);
+                    const int c = scaled_floor<IN>(div_by(v[it][k], denom, rdenom), scale) + 1;
+                    if (live && idx < sym) cpre += c;
+                    if (live && idx == sym) csym = c;
                 }
             }
         }
         if constexpr (MODE == M_DECODE) {
-            lsum += kr_xor<1>(lsum);
-            lsum += kr_xor<2>(lsum);
-            lsum += kr_xor<4>(lsum);
-            if (j == 0 && L < P.n_leaves) sh.leaf_count[L] = lsum;
+            int lc = lsum[it];
+            lc += kr_xor<1>(lc);
+            lc += kr_xor<2>(lc);
+            lc += kr_xor<4>(lc);
+            const int L = it * kLeavesPerIt + wave * 8 + grp;
+            if (j == 0 && L < P.n_leaves) sh.leaf_count[L] = lc;
         }
     }
 
-    // ---- argmax (first maximum) and integer sums across the workgroup ----
-    auto arg_step = [&](float ov, int oi, int oL) {
-        if (better(ov, oi, bp, bi)) { bp = ov; bi = oi; bL = oL; }
-    };
-    arg_step(kr_xor<32>(bp), kr_xor<32>(bi), kr_xor<32>(bL));
-    arg_step(kr_xor<16>(bp), kr_xor<16>(bi), kr_xor<16>(bL));
-    arg_step(kr_xor<8>(bp), kr_xor<8>(bi), kr_xor<8>(bL));
-    arg_step(kr_xor<4>(bp), kr_xor<4>(bi), kr_xor<4>(bL));
-    arg_step(kr_xor<2>(bp), kr_xor<2>(bi), kr_xor<2>(bL));
-    arg_step(kr_xor<1>(bp), kr_xor<1>(bi), kr_xor<1>(bL));
+    // ---- argmax (lowest key) and integer sums across the workgroup ----
+    key = kr_wave_reduce(key, [](int a, int b) { return a < b ? a : b; });
     csum = wave_isum(csum);
     if constexpr (MODE == M_PAIRS) {
         cpre = wave_isum(cpre);
         csym = wave_isum(csym);
     }
     if (lane == 0) {
-        sh.redp[wave] = bp;
-        sh.redi[wave] = bi;
-        sh.redL[wave] = bL;
+        sh.redi[wave] = key;
         sh.redi2[wave] = csum;
         if constexpr (MODE == M_PAIRS) sh.redi3[wave] = cpre;
-        if constexpr (MODE == M_PAIRS) sh.redf[wave] = __int_as_float(csym);
+        if constexpr (MODE == M_PAIRS) sh.redL[wave] = csym;
     }
     __syncthreads();
     if (tid == 0) {
-        float gp = sh.redp[0];
-        int gi = sh.redi[0], gL = sh.redL[0], gs = sh.redi2[0];
+        int gk = sh.redi[0], gs = sh.redi2[0];
         for (int w = 1; w < kWaves; w++) {
-            if (better(sh.redp[w], sh.redi[w], gp, gi)) { gp = sh.redp[w]; gi = sh.redi[w]; gL = sh.redL[w]; }
+            gk = min(gk, sh.redi[w]);
             gs += sh.redi2[w];
         }
-        // A row with no finite maximum (NaN input) has no argmax; bin 0 then
-        // takes the deficit so every index stays in bounds.
-        if (gi < 0 || gi >= V) { gi = 0; gL = 0; }
+        // A row with no maximum (NaN input) has no argmax; bin 0 then takes
+        // the deficit so every index stays in bounds.
+        int gi = gk >> 9, gL = gk & 511;
+        if (gk == 0x7fffffff || gi >= V) { gi = 0; gL = 0; }
         const int deficit = (1 << prec) - gs;
         sh.amax = gi;
         sh.deficit = deficit;
@@ -399,7 +516,7 @@ row_cdf_kernel(const void* __restrict__ input, long long ld, int n_rows, PlanArg
         }
         if constexpr (MODE == M_PAIRS) {
             int pre = 0, cs = 0;
-            for (int w = 0; w < kWaves; w++) { pre += sh.redi3[w]; cs += __float_as_int(sh.redf[w]); }
+            for (int w = 0; w < kWaves; w++) { pre += sh.redi3[w]; cs += sh.redL[w]; }
             const uint32_t lo = (uint32_t)(pre + (gi < sym ? deficit : 0));
             const uint32_t wdt = (uint32_t)(cs + (gi == sym ? deficit : 0));
             reinterpret_cast<uint2*>(out)[row] = make_uint2(lo, lo + wdt);
@@ -463,8 +580,8 @@ row_cdf_kernel(const void* __restrict__ input, long long ld, int n_rows, PlanArg
         __syncthreads();
         const int Lstar = sh.hit_leaf;
         const int gi = sh.amax, deficit = sh.deficit;
-        // The owning lanes recompute the hit leaf's counts from the staged
-        // logits (same operations, same bits) instead of keeping every count.
+        // The owning lanes recompute the hit leaf's counts from the q values
+        // they hold (same operations, same bits) instead of keeping every count.
         #pragma unroll
         for (int it = 0; it < kMaxIt; it++) {
             const int L = it * kLeavesPerIt + wave * 8 + grp;
@@ -475,10 +592,8 @@ row_cdf_kernel(const void* __restrict__ input, long long ld, int n_rows, PlanArg
                     const bool live = k < 16 ? (k < nf) : (j < rm);
                     const int off = k < 16 ? j + 8 * k : 8 * nf + j;
                     if (live) {
-                        const float x = load_val<IN>(rowp, stage, pad, start[it] + off);
-                        const float q = __fmul_rn(kr_kexp(__fsub_rn(x, m)), inv_S);
-                        const float p = div_by(q, denom, rdenom);
-                        const int c = (int)floorf(__fmul_rn(p, scale)) + 1;
+                        const float p = div_by(v[it][k], denom, rdenom);
+                        const int c = scaled_floor<IN>(p, scale) + 1;
                         sh.leaf_buf[off] = c + (start[it] + off == gi ? deficit : 0);
                     }
                 }
@@ -531,6 +646,33 @@ row_cdf_kernel(const void* __restrict__ input, long long ld, int n_rows, PlanArg
                 }
             }
         }
+    }
+}
+
+template <int IN, int MODE>
+__global__ void __launch_bounds__(kThreads)
+row_cdf_kernel(const void* __restrict__ input, long long ld, int n_rows, PlanArgs P, int prec,
+               void* __restrict__ out, long long out_ld, const int32_t* __restrict__ symbols,
+               DecodeArgs D, int async_stage) {
+    __shared__ RowShared sh;
+    __shared__ __attribute__((aligned(16))) kr_half stage[IN == IN_LOGITS_F16 ? kStageMax : 8];
+    const int tid = threadIdx.x;
+    for (int i = tid; i < P.n_inner; i += kThreads) sh.inner[i] = P.inner[i];
+    if (tid <= P.n_levels) sh.level_start[tid] = P.level_start[tid];
+    if (tid < P.n_blocks) sh.roots[tid] = P.roots[tid];
+    const unsigned stage_lds = (unsigned)(uintptr_t)(__attribute__((address_space(3))) char*)stage;
+    if constexpr (MODE == M_PAIRS && IN == IN_LOGITS_F16) {
+        const int G = (int)gridDim.x;
+        int row = (int)blockIdx.x;
+        if (async_stage && row < n_rows)
+            stage_row_async(reinterpret_cast<const kr_half*>(input) + (size_t)row * (size_t)ld, P.V,
+                            stage_lds, tid & 63, tid >> 6);
+        for (; row < n_rows; row += G)
+            cdf_row<IN, MODE>(input, ld, row, row + G < n_rows ? row + G : -1, P, prec, out, out_ld,
+                              symbols, D, sh, stage, stage_lds, async_stage != 0);
+    } else {
+        cdf_row<IN, MODE>(input, ld, (int)blockIdx.x, -1, P, prec, out, out_ld, symbols, D, sh,
+                          stage, stage_lds, false);
     }
 }
 
@@ -610,7 +752,7 @@ int get_plan(int V, PlanArgs* out) {
     std::vector<int2> leaves, inner;
     std::vector<int> level_start, roots;
     const int n_levels = build_plan(V, leaves, inner, level_start, roots);
-    if ((int)leaves.size() > kMaxLeaves)
+    if ((int)leaves.size() > kMaxLeaves || n_levels > kMaxLevels || (int)roots.size() > kMaxBlocks)
         return kr_fail(KR_EUNSUPPORTED, "vocabulary %d too large (max 65536)", V);
     const size_t nb = sizeof(int2) * (leaves.size() + inner.size()) +
                       sizeof(int) * (level_start.size() + roots.size());
@@ -660,8 +802,20 @@ int launch_rows(const void* in, long long ld, int N, int V, int prec, void* out,
     PlanArgs P;
     rc = get_plan(V, &P);
     if (rc) return rc;
-    row_cdf_kernel<IN, MODE><<<N, kThreads, 0, kr_stream(stream)>>>(in, ld, N, P, prec, out,
-                                                                     out_ld, symbols, D);
+    // Pairs (many rows): one persistent workgroup per CU (the stage fills
+    // most of a CU's LDS), each copying its next row in while it computes
+    // the current one. That needs rows whose 16-byte chunks all lie inside
+    // the allocation: 16-byte-aligned rows and a stride that is a multiple of 8.
+    int grid = N, async = 0;
+    if (MODE == M_PAIRS && IN == IN_LOGITS_F16 && ((uintptr_t)in & 15) == 0 && ld % 8 == 0) {
+        int dev = 0, cus = 0;
+        KR_HIP(hipGetDevice(&dev));
+        KR_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+        grid = std::min(N, std::max(cus, 1));
+        async = 1;
+    }
+    row_cdf_kernel<IN, MODE><<<grid, kThreads, 0, kr_stream(stream)>>>(in, ld, N, P, prec, out,
+                                                                        out_ld, symbols, D, async);
     KR_LAUNCHED();
     return KR_OK;
 }

@@ -1,9 +1,10 @@
 // Deterministic float32 exp used by the head softmax.
 //
 // Cody-Waite reduction x = n*ln2 + r (ln2 split into a 15-bit high part and a
-// low part), degree-7 Taylor polynomial of e^r in Horner form, scale by 2^n.
-// Every step is one IEEE-rounded multiply or add (no fma), so the CPU oracle
-// restated with numpy float32 arithmetic produces identical bits. Defined for
+// low part, each step a fused multiply-add), degree-7 Taylor polynomial of
+// e^r in Horner form by fused multiply-adds, scale by 2^n (exact). Every step
+// is one IEEE-rounded operation, so the CPU oracle's C restatement (fmaf,
+// correctly rounded like v_fma_f32) produces identical bits. Defined for
 // x <= 0; inputs below -87 (or NaN / -inf) return 0 so the result is never
 // subnormal.
 #pragma once
@@ -19,18 +20,20 @@
 #define KR_EXP_C3 0x1.555556p-3f
 
 __device__ __forceinline__ float kr_kexp(float x) {
-    if (!(x >= -87.0f)) return 0.0f;
-    const float n = __builtin_rintf(__fmul_rn(x, KR_EXP_LOG2E));
-    const float r = __fsub_rn(__fsub_rn(x, __fmul_rn(n, KR_EXP_LN2_HI)),
-                              __fmul_rn(n, KR_EXP_LN2_LO));
+    // Branch-free: the arithmetic runs on a clamped copy (NaN and -inf become
+    // -87.5, so every intermediate is finite) and the result is selected.
+    const float xc = fmaxf(x, -87.5f);
+    const float n = __builtin_rintf(__fmul_rn(xc, KR_EXP_LOG2E));
+    float r = __builtin_fmaf(-n, KR_EXP_LN2_HI, xc);
+    r = __builtin_fmaf(-n, KR_EXP_LN2_LO, r);
     float p = KR_EXP_C7;
-    p = __fadd_rn(__fmul_rn(p, r), KR_EXP_C6);
-    p = __fadd_rn(__fmul_rn(p, r), KR_EXP_C5);
-    p = __fadd_rn(__fmul_rn(p, r), KR_EXP_C4);
-    p = __fadd_rn(__fmul_rn(p, r), KR_EXP_C3);
-    p = __fadd_rn(__fmul_rn(p, r), 0.5f);
-    p = __fadd_rn(__fmul_rn(p, r), 1.0f);
-    p = __fadd_rn(__fmul_rn(p, r), 1.0f);
-    const int e = (int)n + 127;
-    return __fmul_rn(p, __int_as_float(e << 23));
+    p = __builtin_fmaf(p, r, KR_EXP_C6);
+    p = __builtin_fmaf(p, r, KR_EXP_C5);
+    p = __builtin_fmaf(p, r, KR_EXP_C4);
+    p = __builtin_fmaf(p, r, KR_EXP_C3);
+    p = __builtin_fmaf(p, r, 0.5f);
+    p = __builtin_fmaf(p, r, 1.0f);
+    p = __builtin_fmaf(p, r, 1.0f);
+    const float y = __builtin_ldexpf(p, (int)n);
+    return x >= -87.0f ? y : 0.0f;
 }

@@ -1,7 +1,9 @@
 """ctypes binding of oracle/lib/liboracle_rc.so (TEST INFRASTRUCTURE ONLY).
 
 The C range coder (oracle/range_coder.c) restates krunch_ac/cpu_reference.py
-and is pinned against oracle/range_coder.py in tests/test_oracle_rc.py.
+and is pinned against oracle/range_coder.py in tests/test_oracle_rc.py. The
+same library holds the softmax's exp (oracle/softmax_kexp.c), used by
+oracle/softmax.py and pinned in tests/test_oracle_softmax.py.
 """
 from __future__ import annotations
 
@@ -29,6 +31,8 @@ def lib():
         L.orc_decoder_target.restype = ctypes.c_uint32
         L.orc_decoder_consume.argtypes = [P, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_int]
         L.orc_decode_rows.argtypes = [P, P, ctypes.c_size_t, ctypes.c_uint32, ctypes.c_int, P]
+        L.orc_kexp.argtypes = [P, P, ctypes.c_size_t]
+        L.orc_kexp.restype = None
         _LIB = L
     return _LIB
 

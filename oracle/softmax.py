@@ -7,16 +7,18 @@ fixes every rounding so that CPU and GPU agree bit for bit:
 
   x_i = float32(logit_i)
   m   = max_i x_i
-  e_i = kexp(x_i - m)           # exp2-based exp defined below (no libm)
+  e_i = kexp(x_i - m)           # the exp defined below (no libm exp)
   S   = rowsum_f32(e)           # numpy's float32 row-sum order
   q_i = e_i * (1 / S)           # one IEEE division per row
   cdf = probs_to_cdf(q)         # cdf.py:22-74, bit for bit
 
 `kexp` is a Cody-Waite reduction x = n*ln2 + r, |r| <= ln2/2, followed by the
-degree-7 Taylor polynomial of e^r in Horner form, then scaling by 2^n. Every
-step is a single float32 multiply or add (no fused multiply-add), so numpy's
-float32 arithmetic and the GPU's v_mul_f32/v_add_f32 produce the same bits.
-Inputs below -87 return 0, so the result is never subnormal.
+degree-7 Taylor polynomial of e^r in Horner form, then scaling by 2^n. The
+reduction and every Horner step are fused multiply-adds (one rounding each);
+the multiply by log2(e) and the round to integer are single IEEE operations.
+numpy has no float32 FMA, so kexp is computed by the C restatement in
+`oracle/softmax_kexp.c` (C's fmaf is correctly rounded, as the GPU's
+v_fma_f32 is). Inputs below -87 return 0, so the result is never subnormal.
 
 Pinned by: comparison with float64 exp (<= 2 ulp, tests/test_oracle_softmax.py),
 exact values at 0 and at multiples of ln 2, monotonicity on a dense grid,
@@ -29,26 +31,16 @@ import numpy as np
 from oracle.cdf import probs_to_cdf, CDF_PRECISION
 
 f32 = np.float32
-LOG2E = f32(1.4426950408889634)
-LN2_HI = f32(0.693145751953125)              # 0x3F317200: 15 significant bits
-LN2_LO = f32(0.6931471805599453 - 0.693145751953125)
-EXP_FLOOR = f32(-87.0)
-POLY = [f32(1.0 / 5040.0), f32(1.0 / 720.0), f32(1.0 / 120.0), f32(1.0 / 24.0),
-        f32(1.0 / 6.0), f32(0.5), f32(1.0), f32(1.0)]      # c7 .. c0
 
 
 def kexp(x: np.ndarray) -> np.ndarray:
     """Deterministic float32 exp for x <= 0 (see module docstring)."""
+    from oracle.crc import lib
     x = np.asarray(x, dtype=f32)
-    live = x >= EXP_FLOOR
-    xs = np.where(live, x, f32(0.0)).astype(f32)
-    n = np.rint(xs * LOG2E).astype(f32)
-    r = (xs - n * LN2_HI) - n * LN2_LO
-    poly = np.full_like(r, POLY[0])
-    for c in POLY[1:]:
-        poly = poly * r + c
-    scale = ((n.astype(np.int32) + 127) << 23).astype(np.int32).view(f32)
-    return np.where(live, poly * scale, f32(0.0)).astype(f32)
+    xc = np.ascontiguousarray(x.reshape(-1))
+    out = np.empty_like(xc)
+    lib().orc_kexp(xc.ctypes.data, out.ctypes.data, xc.size)
+    return out.reshape(x.shape)
 
 
 def softmax_probs(logits: np.ndarray) -> np.ndarray:

@@ -92,6 +92,30 @@ def test_pairs_match_oracle_intervals():
     np.testing.assert_array_equal(got[:, 1], hi)
 
 
+@pytest.mark.parametrize("N,V", [(600, 50277), (700, 1000), (300, 5)])
+def test_pairs_persistent_rows_padded_stride(N, V):
+    """Many rows, 8-aligned stride: the persistent path that copies the next
+    row in while computing the current one. The row padding holds values
+    (NaN, +-60000) that must never be read as elements."""
+    ld = (V + 7) // 8 * 8 + 8
+    lg = _logits(N, V, 13, 4.0)
+    full = np.empty((N, ld), dtype=np.float16)
+    full[:, :V] = lg
+    full[:, V:] = np.float16(60000.0)
+    full[::3, V:] = np.float16(np.nan)
+    full[1::3, V:] = np.float16(-60000.0)
+    sym = np.random.default_rng(4).integers(0, V, N).astype(np.int32)
+    d = torch.from_numpy(full).to(DEV)
+    s = torch.from_numpy(sym).to(DEV)
+    pairs = torch.empty((N, 2), dtype=torch.int32, device=DEV)
+    _lib.call("kr_softmax_cdf_pairs", d.data_ptr(), N, V, ld, s.data_ptr(), pairs.data_ptr(), 16,
+              _lib.stream_ptr())
+    lo, hi = osm.sym_intervals(osm.logits_to_cdf(lg, 16), sym)
+    got = pairs.cpu().numpy().view(np.uint32)
+    np.testing.assert_array_equal(got[:, 0], lo)
+    np.testing.assert_array_equal(got[:, 1], hi)
+
+
 def test_fused_decode_matches_oracle():
     """B streams; per step each stream has its own logits row. The oracle
     encodes with the oracle CDFs; the fused kernel decodes from the logits."""
