@@ -15,10 +15,13 @@
 
 #include "kr_model.h"
 
+// ids (nullable): x starts as the embedding of these token ids, gathered by
+// layer 0's LN1-mix, which also writes x.
 int kr_impl_forward_layers(const kr_model_weights* m, void* x, int B, int T, void* state,
-                           void* ws, size_t ws_bytes, hipStream_t s);
+                           void* ws, size_t ws_bytes, hipStream_t s, const int32_t* ids);
 int kr_impl_forward_layers_view(const kr_model_weights* m, void* x, int B, int T, void* state,
-                                int state_B, int b0, void* ws, size_t ws_bytes, hipStream_t s);
+                                int state_B, int b0, void* ws, size_t ws_bytes, hipStream_t s,
+                                const int32_t* ids);
 int kr_impl_embed(const kr_model_weights* m, const int32_t* ids, int M, void* x, hipStream_t s);
 int kr_impl_head(const kr_model_weights* m, const void* x, int M, void* xn, void* logits,
                  long long ld, hipStream_t s);
@@ -86,9 +89,8 @@ struct DecodeStepArgs {
 };
 
 int decode_step(const DecodeStepArgs& a, hipStream_t s) {
-    KR_TRY(kr_impl_embed(a.m, a.syms, a.B, a.x, s));
     KR_TRY(kr_impl_forward_layers_view(a.m, a.x, a.B, 1, a.state, a.state_B, a.b0, a.ws,
-                                       a.ws_bytes, s));
+                                       a.ws_bytes, s, a.syms));
     void* xn = kr_impl_head_scratch(a.ws, a.B, a.m->C, a.m->F);
     KR_TRY(kr_impl_head(a.m, a.x, a.B, xn, a.logits, a.ld, s));
     return kr_softmax_cdf_decode(reinterpret_cast<const uint16_t*>(a.logits), a.B, a.m->V, a.ld,
@@ -120,7 +122,7 @@ size_t kr_forward_workspace_bytes(long long M, int C, int F) {
 
 int kr_forward_layers(const kr_model_weights* m, void* x, int B, int T, void* state, void* ws,
                       size_t ws_bytes, void* stream) {
-    return kr_impl_forward_layers(m, x, B, T, state, ws, ws_bytes, kr_stream(stream));
+    return kr_impl_forward_layers(m, x, B, T, state, ws, ws_bytes, kr_stream(stream), nullptr);
 }
 
 int kr_embed(const kr_model_weights* m, const int32_t* ids, int M, void* x, void* stream) {
@@ -144,8 +146,7 @@ int kr_compress_window(const kr_model_weights* m, const int32_t* inputs, const i
     const long long M = (long long)B * T;
     KR_REQUIRE(ws_bytes >= kr_impl_work_bytes(M, m->C, m->F), "kr_compress_window: workspace too small");
     hipStream_t s = kr_stream(stream);
-    KR_TRY(kr_impl_embed(m, inputs, (int)M, x, s));
-    KR_TRY(kr_impl_forward_layers(m, x, B, T, state, ws, ws_bytes, s));
+    KR_TRY(kr_impl_forward_layers(m, x, B, T, state, ws, ws_bytes, s, inputs));
     void* xn = kr_impl_head_scratch(ws, M, m->C, m->F);
     for (long long r0 = 0; r0 < M; r0 += head_rows) {
         const int n = (int)((M - r0) < head_rows ? (M - r0) : head_rows);

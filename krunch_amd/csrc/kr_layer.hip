@@ -60,6 +60,12 @@ __device__ __forceinline__ void load_coef(const kr_half* __restrict__ p, int lan
 }
 
 template <int G>
+__device__ __forceinline__ void store_coef(kr_half* __restrict__ p, int lane, const CoefH<G>& c) {
+    #pragma unroll
+    for (int i = 0; i < G; i++) *reinterpret_cast<kr_half4*>(p + 256 * i + 4 * lane) = c.v[i];
+}
+
+template <int G>
 __device__ __forceinline__ void to_float(const CoefH<G>& h, RowF<G>& r) {
     #pragma unroll
     for (int i = 0; i < G; i++)
@@ -174,6 +180,13 @@ struct LnMixArgs {
     int frag;                  // mix outputs fragment-packed (small-M GEMM operands)
     int8_t* q[3];              // w8a8: NMIX int8 outputs instead of out[] (per-row quantised)
     float* qs[3];              // w8a8: their per-row scales
+    // Embedding gather fused in (layer 0): row r of x is emb[ids[r]] (ids
+    // clamped into [0, V), as embed_kernel does), read from the table and
+    // also written to xw, the residual stream the later products add onto.
+    const int32_t* ids;
+    const kr_half* emb;
+    int V;
+    kr_half* xw;
 };
 
 // One wave per run of `run` consecutive tokens of one stream. The wave that
@@ -201,19 +214,27 @@ __global__ void __launch_bounds__(256) ln_mix_kernel(LnMixArgs a) {
         #pragma unroll
         for (int m = 0; m < NMIX; m++) load_coef<G>(a.tm[m], lane, tm[m]);
     }
+    // source of row r of x: the residual stream, or the embedding table
+    auto xrow = [&](size_t r) -> const kr_half* {
+        if (!a.ids) return a.x + r * C;
+        int id = a.ids[r];
+        id = id < 0 ? 0 : (id >= a.V ? a.V - 1 : id);
+        return a.emb + (size_t)id * C;
+    };
     // the first row and the row shifted in ahead of it, both in flight at once
     CoefH<G> prev_h, first_h;
     if constexpr (NMIX > 0)
-        load_coef<G>(t0 == 0 ? a.state + (size_t)b * C : a.x + (row0 + t0 - 1) * C, lane, prev_h);
-    load_coef<G>(a.x + (row0 + t0) * C, lane, first_h);
+        load_coef<G>(t0 == 0 ? a.state + (size_t)b * C : xrow(row0 + t0 - 1), lane, prev_h);
+    load_coef<G>(xrow(row0 + t0), lane, first_h);
     RowF<G> prev, cur;
     if constexpr (NMIX > 0) {
         to_float<G>(prev_h, prev);
         if (t0 != 0) layer_norm_row<G>(prev, w, bias);
     }
     for (int t = t0; t < t1; t++) {
-        if (t == t0) to_float<G>(first_h, cur);
-        else load_row<G>(a.x + (row0 + t) * C, lane, cur);
+        if (t != t0) load_coef<G>(xrow(row0 + t), lane, first_h);
+        if (a.ids) store_coef<G>(a.xw + (row0 + t) * C, lane, first_h);
+        to_float<G>(first_h, cur);
         layer_norm_row<G>(cur, w, bias);
         if constexpr (NMIX == 0) {
             store_row<G>(a.out[0] + (row0 + t) * C, lane, cur);
@@ -229,7 +250,7 @@ __global__ void __launch_bounds__(256) ln_mix_kernel(LnMixArgs a) {
     if constexpr (NMIX > 0) {
         if (t0 == 0) {
             if (t1 < a.T) {
-                load_row<G>(a.x + (row0 + a.T - 1) * C, lane, cur);
+                load_row<G>(xrow(row0 + a.T - 1), lane, cur);
                 layer_norm_row<G>(cur, w, bias);
             }
             store_row<G>(a.state + (size_t)b * C, lane, cur);
@@ -645,8 +666,24 @@ kr_gemm_args gemm_q8(const int8_t* A, const float* sa, int M, int K, const kr_ma
     return g;
 }
 
+// Layer 0 of a forward that starts from token ids: its LN1-mix gathers the
+// embedding rows itself and writes x (no separate embed launch).
+struct EmbedSrc {
+    const int32_t* ids;
+    const kr_half* emb;
+    int V;
+};
+
+inline void set_embed(LnMixArgs& a, const EmbedSrc* e, kr_half* x) {
+    a.ids = e ? e->ids : nullptr;
+    a.emb = e ? e->emb : nullptr;
+    a.V = e ? e->V : 0;
+    a.xw = e ? x : nullptr;
+}
+
 int layer_forward_q8(const kr_layer_weights& L, int C, int F, kr_half* x, int B, int T,
-                     const kr_layer_state& st, const Work& w, hipStream_t s) {
+                     const kr_layer_state& st, const Work& w, hipStream_t s,
+                     const EmbedSrc* e) {
     const kr_layer_q8& Q = *L.q8;
     const int M = B * T, G = C / 256;
     const bool fr = M <= KR_GEMM_SMALL_M && Q.K.qf && Q.V.qf && Q.R.qf && Q.O.qf && Q.fK.qf &&
@@ -663,7 +700,9 @@ int layer_forward_q8(const kr_layer_weights& L, int C, int F, kr_half* x, int B,
     a.T = T;
     a.run = rows_per_run(T);
     a.frag = fr ? 1 : 0;
+    set_embed(a, e, x);
     KR_TRY(launch_ln_mix<3>(G, a, s));
+    set_embed(a, nullptr, x);
     {
         const kr_gemm_args jobs[3] = {gemm_q8(w.kx8, w.kxs, M, C, Q.K, C, w.k, fr),
                                       gemm_q8(w.vx8, w.vxs, M, C, Q.V, C, w.v, fr),
@@ -701,7 +740,8 @@ int layer_forward_q8(const kr_layer_weights& L, int C, int F, kr_half* x, int B,
 // K, V, R products fused with WKV, the output projection, LN2-mix and the
 // channel mix (six launches).
 int layer_step_fused(const kr_layer_weights& L, int C, int F, kr_half* x, int B,
-                     const kr_layer_state& st, const Work& w, hipStream_t s) {
+                     const kr_layer_state& st, const Work& w, hipStream_t s,
+                     const EmbedSrc* e) {
     const int M = B, G = C / 256;
     LnMixArgs a{};
     a.x = x;
@@ -714,7 +754,9 @@ int layer_step_fused(const kr_layer_weights& L, int C, int F, kr_half* x, int B,
     a.T = 1;
     a.run = 1;
     a.frag = 1;
+    set_embed(a, e, x);
     KR_TRY(launch_ln_mix<3>(G, a, s));
+    set_embed(a, nullptr, x);
     KvrWkvArgs kw{};
     kw.A[0] = w.kx; kw.A[1] = w.vx; kw.A[2] = w.rx;
     kw.Wf[0] = H(L.Kf); kw.Wf[1] = H(L.Vf); kw.Wf[2] = H(L.Rf);
@@ -745,11 +787,12 @@ int layer_step_fused(const kr_layer_weights& L, int C, int F, kr_half* x, int B,
 }
 
 int layer_forward(const kr_layer_weights& L, int C, int F, kr_half* x, int B, int T,
-                  const kr_layer_state& st, const Work& w, hipStream_t s) {
-    if (L.q8) return layer_forward_q8(L, C, F, x, B, T, st, w, s);
+                  const kr_layer_state& st, const Work& w, hipStream_t s,
+                  const EmbedSrc* e = nullptr) {
+    if (L.q8) return layer_forward_q8(L, C, F, x, B, T, st, w, s, e);
     const int M = B * T, G = C / 256;
     const bool fr = use_fragments(L, M);
-    if (fr && T == 1) return layer_step_fused(L, C, F, x, B, st, w, s);
+    if (fr && T == 1) return layer_step_fused(L, C, F, x, B, st, w, s, e);
     LnMixArgs a{};
     a.x = x;
     a.ln_w = H(L.ln1_w);
@@ -761,7 +804,9 @@ int layer_forward(const kr_layer_weights& L, int C, int F, kr_half* x, int B, in
     a.T = T;
     a.run = rows_per_run(T);
     a.frag = fr ? 1 : 0;
+    set_embed(a, e, x);
     KR_TRY(launch_ln_mix<3>(G, a, s));
+    set_embed(a, nullptr, x);
     {
         const kr_gemm_args jobs[3] = {
             gemm_args(w.kx, M, C, L.Kt, C, w.k, nullptr, nullptr, L.Kf, fr),
@@ -820,24 +865,28 @@ kr_layer_state state_of(void* state, int layer, int B, int C) {
 }  // namespace
 
 // Entry points used by kr_engine.cpp.
+// ids (nullable): x starts as the embedding of these [B, T] token ids, gathered
+// by layer 0's LN1-mix (which writes x); otherwise x holds the input rows.
 int kr_impl_forward_layers(const kr_model_weights* m, void* x, int B, int T, void* state,
-                           void* ws, size_t ws_bytes, hipStream_t s) {
+                           void* ws, size_t ws_bytes, hipStream_t s, const int32_t* ids) {
     KR_TRY(check_model(m));
     KR_REQUIRE(x && state && ws, "forward: null pointer");
     const long long M = (long long)B * T;
     KR_REQUIRE(B >= 1 && T >= 1 && M <= (1ll << 31) / m->F, "forward: bad B=%d T=%d", B, T);
     KR_REQUIRE(ws_bytes >= work_bytes(M, m->C, m->F), "forward: workspace too small");
     const Work w = carve(ws, M, m->C, m->F);
+    const EmbedSrc e{ids, H(m->emb), m->V};
     for (int i = 0; i < m->n_layer; i++)
         KR_TRY(layer_forward(m->layers[i], m->C, m->F, Hm(x), B, T, state_of(state, i, B, m->C),
-                             w, s));
+                             w, s, i == 0 && ids ? &e : nullptr));
     return KR_OK;
 }
 
 // The layer stack for streams [b0, b0 + B) of a state buffer holding state_B
 // streams (one group of a larger batch; rows of each [state_B, C] component).
 int kr_impl_forward_layers_view(const kr_model_weights* m, void* x, int B, int T, void* state,
-                                int state_B, int b0, void* ws, size_t ws_bytes, hipStream_t s) {
+                                int state_B, int b0, void* ws, size_t ws_bytes, hipStream_t s,
+                                const int32_t* ids) {
     KR_TRY(check_model(m));
     KR_REQUIRE(x && state && ws, "forward: null pointer");
     KR_REQUIRE(b0 >= 0 && B >= 1 && b0 + B <= state_B, "forward: bad stream range");
@@ -846,6 +895,7 @@ int kr_impl_forward_layers_view(const kr_model_weights* m, void* x, int B, int T
     KR_REQUIRE(ws_bytes >= work_bytes(M, m->C, m->F), "forward: workspace too small");
     const Work w = carve(ws, M, m->C, m->F);
     const size_t off = (size_t)b0 * m->C;
+    const EmbedSrc e{ids, H(m->emb), m->V};
     for (int i = 0; i < m->n_layer; i++) {
         kr_layer_state st = state_of(state, i, state_B, m->C);
         st.att_xx = static_cast<kr_half*>(st.att_xx) + off;
@@ -853,7 +903,8 @@ int kr_impl_forward_layers_view(const kr_model_weights* m, void* x, int B, int T
         st.aa += off;
         st.bb += off;
         st.pp += off;
-        KR_TRY(layer_forward(m->layers[i], m->C, m->F, Hm(x), B, T, st, w, s));
+        KR_TRY(layer_forward(m->layers[i], m->C, m->F, Hm(x), B, T, st, w, s,
+                             i == 0 && ids ? &e : nullptr));
     }
     return KR_OK;
 }
