@@ -129,6 +129,16 @@ def kernel_probe(weights16, B):
         _lib.call("kr_softmax_cdf_pairs", logits.data_ptr(), rows, P.V, ld, syms.data_ptr(),
                   pairs.data_ptr(), 24, s)
     torch.cuda.synchronize()
+    # the fused CDF search + range decode of one decode step (B rows; zeroed
+    # decoder states over a zeroed stream are valid inputs)
+    buf = torch.zeros(1 << 16, dtype=torch.uint8, device=dev)
+    states = torch.zeros(4 * B, dtype=torch.int32, device=dev)
+    out_syms = torch.empty(B, dtype=torch.int32, device=dev)
+    for _ in range(2):
+        _lib.call("kr_softmax_cdf_decode", logits.data_ptr(), B, P.V, ld, buf.data_ptr(),
+                  buf.numel(), None, None, states.data_ptr(), out_syms.data_ptr(), None, 0, None,
+                  None, 16, s)
+    torch.cuda.synchronize()
     print(json.dumps({"probe": "ok", "copy_bytes": 2 * src.numel() * 4}))
 
 
