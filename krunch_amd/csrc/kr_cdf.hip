@@ -21,6 +21,7 @@
 // find the symbol whose interval contains a range decoder's target and
 // advance the decoder (decompress, fused).
 #include <cstring>
+#include <functional>
 #include <map>
 #include <mutex>
 #include <vector>
@@ -49,6 +50,7 @@ struct PlanArgs {
     const int2* inner;       // (left, right) node ids, grouped by level
     const int* level_start;  // n_levels + 1 offsets into inner
     const int* roots;        // node id of each 8192-block
+    const int* wave_root;    // [kMaxIt * kWaves]: node id of the 8-leaf subtree a wave sums itself, or -1
     int V, n_leaves, n_inner, n_levels, n_blocks;
 };
 
@@ -70,6 +72,7 @@ struct RowShared {
     int2 inner[kMaxLeaves];                  // the summation plan, copied once
     int level_start[kMaxLevels + 1];
     int roots[kMaxBlocks];
+    int wave_root[kMaxIt * kWaves];
     int leaf_count[kMaxLeaves];
     int leaf_buf[128];
     float redf[kWaves];
@@ -166,11 +169,15 @@ __device__ __forceinline__ float row_shl(float v) {
 // a signed zero can only decide the sign of a partial sum that is exactly
 // zero, which then adds exactly into any nonzero sum, so only an all-zero
 // row can differ (in the sign of its zero total).
+// act[it]: the wave holds leaves in register slice it; tail[it]: some leaf
+// of the wave's slice has a len % 8 tail (both wave-uniform).
 __device__ float row_sum_numpy(const float (&v)[kMaxIt][17], const int (&len)[kMaxIt],
+                               const bool (&act)[kMaxIt], const bool (&tail)[kMaxIt],
                                const PlanArgs& P, RowShared& sh, int lane, int wave) {
     const int grp = lane >> 3, j = lane & 7;
     #pragma unroll
     for (int it = 0; it < kMaxIt; it++) {
+        if (!act[it]) continue;
         float r = v[it][0];
         #pragma unroll
         for (int k = 1; k < 16; k++) r = r + v[it][k];
@@ -178,30 +185,53 @@ __device__ float row_sum_numpy(const float (&v)[kMaxIt][17], const int (&len)[kM
         r = r + kr_xor<2>(r);
         r = r + kr_xor<4>(r);
         // the len % 8 tail elements, in order, onto lane 0 of the group
-        const float t = v[it][16];
         float res = len[it] >= 8 ? r : -0.0f;
-        res = res + t;
-        res = res + row_shl<1>(t);
-        res = res + row_shl<2>(t);
-        res = res + row_shl<3>(t);
-        res = res + row_shl<4>(t);
-        res = res + row_shl<5>(t);
-        res = res + row_shl<6>(t);
+        if (tail[it]) {
+            const float t = v[it][16];
+            res = res + t;
+            res = res + row_shl<1>(t);
+            res = res + row_shl<2>(t);
+            res = res + row_shl<3>(t);
+            res = res + row_shl<4>(t);
+            res = res + row_shl<5>(t);
+            res = res + row_shl<6>(t);
+        }
         const int L = it * kLeavesPerIt + wave * 8 + grp;
-        if (j == 0 && L < P.n_leaves) sh.node[L] = res;
+        const int wr = sh.wave_root[it * kWaves + wave];   // wave-uniform
+        if (wr >= 0) {
+            // The wave's 8 leaves form a perfect subtree of the plan: its
+            // three levels are the pairs (lane, lane ^ 8), ^ 16, ^ 32 of the
+            // groups' lane 0 (left + right == right + left in IEEE).
+            res = res + kr_xor<8>(res);
+            res = res + kr_xor<16>(res);
+            res = res + kr_xor<32>(res);
+            if (lane == 0) sh.node[wr] = res;
+        } else if (j == 0 && L < P.n_leaves) {
+            sh.node[L] = res;
+        }
     }
     __syncthreads();
     // Inner nodes level by level, then the blocks left to right, by wave 0
     // alone: a wave's LDS accesses execute in program order, so each level
-    // reads the previous one's writes without a workgroup barrier.
+    // reads the previous one's writes without a workgroup barrier. The next
+    // level's child pairs are read ahead (levels hold <= 64 nodes at V <=
+    // 65536; a larger level takes the loop).
     if (wave == 0) {
+        int s = sh.level_start[0];
+        int e = P.n_levels > 0 ? sh.level_start[1] : s;
+        int2 ch = lane < e - s ? sh.inner[s + lane] : make_int2(0, 0);
         for (int lev = 0; lev < P.n_levels; lev++) {
-            const int s = sh.level_start[lev], e = sh.level_start[lev + 1];
-            for (int idx = s + lane; idx < e; idx += 64) {
-                const int2 ch = sh.inner[idx];
-                sh.node[P.n_leaves + idx] = sh.node[ch.x] + sh.node[ch.y];
+            const int e2 = lev + 1 < P.n_levels ? sh.level_start[lev + 2] : e;
+            const int2 nxt = lane < e2 - e ? sh.inner[e + lane] : make_int2(0, 0);
+            if (lane < e - s) sh.node[P.n_leaves + s + lane] = sh.node[ch.x] + sh.node[ch.y];
+            for (int idx = s + 64 + lane; idx < e; idx += 64) {
+                const int2 c2 = sh.inner[idx];
+                sh.node[P.n_leaves + idx] = sh.node[c2.x] + sh.node[c2.y];
             }
             __builtin_amdgcn_wave_barrier();
+            ch = nxt;
+            s = e;
+            e = e2;
         }
         if (lane == 0) {
             float acc = 0.0f;
@@ -264,7 +294,8 @@ __device__ __forceinline__ void cdf_row(const void* __restrict__ input, long lon
                                         const int32_t* __restrict__ symbols, const DecodeArgs& D,
                                         RowShared& sh, kr_half* stage, unsigned stage_lds,
                                         bool async_stage) {
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int grp = lane >> 3, j = lane & 7;
     const int V = P.V;
 
@@ -310,14 +341,20 @@ __device__ __forceinline__ void cdf_row(const void* __restrict__ input, long lon
     // element get -inf (softmax input, and the argmax of probabilities) ----
     float v[kMaxIt][17];
     int start[kMaxIt], len[kMaxIt];
+    // Slices past the row's leaves (a whole wave's, e.g. the last slice for
+    // most waves at V = 50277) and tail slots of full leaves are skipped in
+    // every phase: their slots would only carry zeros.
+    bool act[kMaxIt], tail[kMaxIt];
     #pragma unroll
     for (int it = 0; it < kMaxIt; it++) {
         const int L = it * kLeavesPerIt + wave * 8 + grp;
+        act[it] = it * kLeavesPerIt + wave * 8 < P.n_leaves;
         int2 lf = make_int2(0, 0);
         if (L < P.n_leaves) lf = P.leaves[L];
         start[it] = lf.x;
         len[it] = lf.y;
         const int nf = leaf_full(lf.y), rm = leaf_rem(lf.y);
+        tail[it] = __ballot(j < rm) != 0;
         if constexpr (IN == IN_LOGITS_F16) {
             // A leaf inside one 128-element skew segment (every leaf of a
             // full 8192-element block) reads at one constant offset. Slots
@@ -352,8 +389,10 @@ __device__ __forceinline__ void cdf_row(const void* __restrict__ input, long lon
     float m = -INFINITY;
     #pragma unroll
     for (int it = 0; it < kMaxIt; it++)
-        #pragma unroll
-        for (int k = 0; k < 17; k++) m = fmaxf(m, v[it][k]);
+        if (act[it]) {
+            #pragma unroll
+            for (int k = 0; k < 17; k++) m = fmaxf(m, v[it][k]);
+        }
     m = wave_max(m);
     if (lane == 0) sh.redf[wave] = m;
     __syncthreads();
@@ -372,22 +411,30 @@ __device__ __forceinline__ void cdf_row(const void* __restrict__ input, long lon
         // ---- e = kexp(x - m); S = numpy-order sum; q = e * (1/S) ----
         #pragma unroll
         for (int it = 0; it < kMaxIt; it++)
-            #pragma unroll
-            for (int k = 0; k < 17; k++) v[it][k] = kr_kexp(__fsub_rn(v[it][k], m));
-        const float S = row_sum_numpy(v, len, P, sh, lane, wave);
+            if (act[it]) {
+                #pragma unroll
+                for (int k = 0; k < 16; k++) v[it][k] = kr_kexp(__fsub_rn(v[it][k], m));
+                v[it][16] = tail[it] ? kr_kexp(__fsub_rn(v[it][16], m)) : 0.0f;
+            }
+        const float S = row_sum_numpy(v, len, act, tail, P, sh, lane, wave);
         inv_S = 1.0f / S;
         #pragma unroll
         for (int it = 0; it < kMaxIt; it++)
-            #pragma unroll
-            for (int k = 0; k < 17; k++) v[it][k] = __fmul_rn(v[it][k], inv_S);
+            if (act[it]) {
+                #pragma unroll
+                for (int k = 0; k < 16; k++) v[it][k] = __fmul_rn(v[it][k], inv_S);
+                if (tail[it]) v[it][16] = __fmul_rn(v[it][16], inv_S);
+            }
         // every e <= kexp(0) = 1, reached at the maximum logit
         qmax = inv_S;
     } else {
         qmax = m;
         #pragma unroll
         for (int it = 0; it < kMaxIt; it++)
-            #pragma unroll
-            for (int k = 0; k < 17; k++) if (v[it][k] == -INFINITY) v[it][k] = 0.0f;
+            if (act[it]) {
+                #pragma unroll
+                for (int k = 0; k < 17; k++) if (v[it][k] == -INFINITY) v[it][k] = 0.0f;
+            }
     }
 
     if constexpr (MODE == M_PROBS) {
@@ -404,7 +451,7 @@ __device__ __forceinline__ void cdf_row(const void* __restrict__ input, long lon
     }
 
     // ---- cdf.py: p = q / max(sum(q), 1e-30) ----
-    const float P_sum = row_sum_numpy(v, len, P, sh, lane, wave);
+    const float P_sum = row_sum_numpy(v, len, act, tail, P, sh, lane, wave);
     const float denom = fmaxf(P_sum, 1e-30f);
     const float rdenom = 1.0f / denom;
     const float scale = (float)((1 << prec) - V);
@@ -425,8 +472,11 @@ __device__ __forceinline__ void cdf_row(const void* __restrict__ input, long lon
     for (int it = kMaxIt - 1; it >= 0; it--) {
         const int nf = leaf_full(len[it]), rm = leaf_rem(len[it]);
         int ls = 0;
+        lsum[it] = 0;
+        if (!act[it]) continue;
         #pragma unroll
         for (int k = 16; k >= 0; k--) {
+            if (k == 16 && !tail[it]) continue;   // no lane holds a tail element
             const float p = div_by(v[it][k], denom, rdenom);
             const int f = scaled_floor<IN>(p, scale);
             ls += f;
@@ -660,6 +710,7 @@ row_cdf_kernel(const void* __restrict__ input, long long ld, int n_rows, PlanArg
     for (int i = tid; i < P.n_inner; i += kThreads) sh.inner[i] = P.inner[i];
     if (tid <= P.n_levels) sh.level_start[tid] = P.level_start[tid];
     if (tid < P.n_blocks) sh.roots[tid] = P.roots[tid];
+    if (tid < kMaxIt * kWaves) sh.wave_root[tid] = P.wave_root[tid];
     const unsigned stage_lds = (unsigned)(uintptr_t)(__attribute__((address_space(3))) char*)stage;
     if constexpr (MODE == M_PAIRS && IN == IN_LOGITS_F16) {
         const int G = (int)gridDim.x;
@@ -689,58 +740,104 @@ std::map<std::pair<int, int>, DevPlan> g_plans;
 
 struct BuildNode { bool leaf; int id; };
 
+// The plan of numpy's pairwise summation of a row of V elements: leaves
+// (start, len) in index order, inner nodes (left, right) grouped by level,
+// the root of each 8192-element block, and for each (register slice, wave)
+// the node whose 8-leaf subtree that wave sums in registers (-1: none).
+// Node ids: leaves 0..NL-1, then the LDS-summed inner nodes in level order,
+// then the wave-summed subtree roots. Returns the number of levels.
 int build_plan(int V, std::vector<int2>& leaves, std::vector<int2>& inner_out,
-               std::vector<int>& level_start, std::vector<int>& roots) {
-    struct Inner { BuildNode l, r; int height; };
+               std::vector<int>& level_start, std::vector<int>& roots, std::vector<int>& wave_root) {
+    struct Inner { BuildNode l, r; };
     std::vector<Inner> inner;
-    std::vector<int> leaf_height;
     // recursive split, numpy pairwise rule
     struct Rec {
         std::vector<int2>& leaves;
         std::vector<Inner>& inner;
-        std::pair<BuildNode, int> go(int start, int n) {
+        BuildNode go(int start, int n) {
             if (n <= 128) {
                 leaves.push_back(make_int2(start, n));
-                return {BuildNode{true, (int)leaves.size() - 1}, 0};
+                return BuildNode{true, (int)leaves.size() - 1};
             }
             int half = n / 2;
             half -= half % 8;
-            auto l = go(start, half);
-            auto r = go(start + half, n - half);
-            const int h = 1 + std::max(l.second, r.second);
-            inner.push_back(Inner{l.first, r.first, h});
-            return {BuildNode{false, (int)inner.size() - 1}, h};
+            const BuildNode l = go(start, half);
+            const BuildNode r = go(start + half, n - half);
+            inner.push_back(Inner{l, r});
+            return BuildNode{false, (int)inner.size() - 1};
         }
     } rec{leaves, inner};
     std::vector<BuildNode> block_roots;
-    for (int s = 0; s < V; s += 8192) block_roots.push_back(rec.go(s, std::min(8192, V - s)).first);
+    for (int s = 0; s < V; s += 8192) block_roots.push_back(rec.go(s, std::min(8192, V - s)));
     const int NL = (int)leaves.size(), NI = (int)inner.size();
-    // order inner nodes by height (children always have smaller height)
-    std::vector<int> order(NI);
-    for (int i = 0; i < NI; i++) order[i] = i;
-    std::stable_sort(order.begin(), order.end(),
-                     [&](int a, int b) { return inner[a].height < inner[b].height; });
-    std::vector<int> pos(NI);
-    for (int i = 0; i < NI; i++) pos[order[i]] = i;
-    auto ident = [&](BuildNode n) { return n.leaf ? n.id : NL + pos[n.id]; };
-    inner_out.resize(NI);
-    int max_h = 0;
-    for (int i = 0; i < NI; i++) {
-        const Inner& in = inner[order[i]];
-        inner_out[i] = make_int2(ident(in.l), ident(in.r));
-        max_h = std::max(max_h, in.height);
+    auto key = [](BuildNode n) { return n.leaf ? (long long)n.id : -(long long)n.id - 1; };
+    std::map<std::pair<long long, long long>, int> by_children;
+    for (int i = 0; i < NI; i++) by_children[{key(inner[i].l), key(inner[i].r)}] = i;
+    auto find = [&](BuildNode a, BuildNode b) -> int {
+        auto f = by_children.find({key(a), key(b)});
+        return f == by_children.end() ? -1 : f->second;
+    };
+    // 0: summed in LDS, 1: inside a wave subtree, 2: root of a wave subtree
+    std::vector<int> kind(NI, 0);
+    std::vector<int> wave_node(kMaxIt * kWaves, -1);
+    for (int it = 0; it < kMaxIt; it++)
+        for (int w = 0; w < kWaves; w++) {
+            const int L0 = it * kLeavesPerIt + w * 8;
+            if (L0 + 7 >= NL) continue;
+            int lvl[4], cnt = 4;
+            bool ok = true;
+            std::vector<int> internal;
+            for (int k = 0; k < 4 && ok; k++)
+                ok = (lvl[k] = find(BuildNode{true, L0 + 2 * k}, BuildNode{true, L0 + 2 * k + 1})) >= 0;
+            while (ok && cnt > 1) {
+                for (int k = 0; k < cnt / 2 && ok; k++) {
+                    internal.push_back(lvl[2 * k]);
+                    internal.push_back(lvl[2 * k + 1]);
+                    ok = (lvl[k] = find(BuildNode{false, lvl[2 * k]}, BuildNode{false, lvl[2 * k + 1]})) >= 0;
+                }
+                cnt /= 2;
+            }
+            if (!ok) continue;   // only a complete subtree of 8 leaves counts
+            for (int n : internal) kind[n] = 1;
+            kind[lvl[0]] = 2;
+            wave_node[it * kWaves + w] = lvl[0];
+        }
+    // levels of the LDS-summed nodes (leaves and wave roots are level 0)
+    std::vector<int> level(NI, -1);
+    std::function<int(BuildNode)> lev_of = [&](BuildNode n) -> int {
+        if (n.leaf || kind[n.id] == 2) return 0;
+        if (level[n.id] >= 0) return level[n.id];
+        return level[n.id] = 1 + std::max(lev_of(inner[n.id].l), lev_of(inner[n.id].r));
+    };
+    std::vector<int> order;
+    for (int i = 0; i < NI; i++)
+        if (kind[i] == 0) { lev_of(BuildNode{false, i}); order.push_back(i); }
+    std::stable_sort(order.begin(), order.end(), [&](int a, int b) { return level[a] < level[b]; });
+    std::vector<int> id(NI, -1);
+    for (int i = 0; i < (int)order.size(); i++) id[order[i]] = NL + i;
+    int next = NL + (int)order.size();
+    for (int i = 0; i < NI; i++) if (kind[i] == 2) id[i] = next++;
+    auto ident = [&](BuildNode n) { return n.leaf ? n.id : id[n.id]; };
+    inner_out.resize(order.size());
+    int max_l = 0;
+    for (int i = 0; i < (int)order.size(); i++) {
+        inner_out[i] = make_int2(ident(inner[order[i]].l), ident(inner[order[i]].r));
+        max_l = std::max(max_l, level[order[i]]);
     }
-    level_start.assign(max_h + 1, 0);
+    level_start.assign(max_l + 1, 0);
     {
         int idx = 0;
-        for (int h = 1; h <= max_h; h++) {
+        for (int h = 1; h <= max_l; h++) {
             level_start[h - 1] = idx;
-            while (idx < NI && inner[order[idx]].height == h) idx++;
+            while (idx < (int)order.size() && level[order[idx]] == h) idx++;
         }
-        level_start[max_h] = idx;
+        level_start[max_l] = idx;
     }
     for (auto& r : block_roots) roots.push_back(ident(r));
-    return max_h;
+    wave_root.assign(kMaxIt * kWaves, -1);
+    for (int x = 0; x < kMaxIt * kWaves; x++)
+        if (wave_node[x] >= 0) wave_root[x] = id[wave_node[x]];
+    return max_l;
 }
 
 int get_plan(int V, PlanArgs* out) {
@@ -750,12 +847,14 @@ int get_plan(int V, PlanArgs* out) {
     auto it = g_plans.find({dev, V});
     if (it != g_plans.end()) { *out = it->second.args; return KR_OK; }
     std::vector<int2> leaves, inner;
-    std::vector<int> level_start, roots;
-    const int n_levels = build_plan(V, leaves, inner, level_start, roots);
+    std::vector<int> level_start, roots, wave_root;
+    const int n_levels = build_plan(V, leaves, inner, level_start, roots, wave_root);
     if ((int)leaves.size() > kMaxLeaves || n_levels > kMaxLevels || (int)roots.size() > kMaxBlocks)
-        return kr_fail(KR_EUNSUPPORTED, "vocabulary %d too large (max 65536)", V);
+        return kr_fail(KR_EUNSUPPORTED,
+                       "vocabulary %d needs %d summation leaves, %d levels (max %d, %d)", V,
+                       (int)leaves.size(), n_levels, kMaxLeaves, kMaxLevels);
     const size_t nb = sizeof(int2) * (leaves.size() + inner.size()) +
-                      sizeof(int) * (level_start.size() + roots.size());
+                      sizeof(int) * (level_start.size() + roots.size() + wave_root.size());
     std::vector<char> host(nb);
     char* p = host.data();
     auto put = [&](const void* src, size_t bytes) { std::memcpy(p, src, bytes); p += bytes; };
@@ -763,6 +862,7 @@ int get_plan(int V, PlanArgs* out) {
     put(inner.data(), sizeof(int2) * inner.size());
     put(level_start.data(), sizeof(int) * level_start.size());
     put(roots.data(), sizeof(int) * roots.size());
+    put(wave_root.data(), sizeof(int) * wave_root.size());
     void* mem = nullptr;
     KR_HIP(hipMalloc(&mem, nb));
     KR_HIP(hipMemcpy(mem, host.data(), nb, hipMemcpyHostToDevice));
@@ -775,6 +875,8 @@ int get_plan(int V, PlanArgs* out) {
     a.level_start = reinterpret_cast<const int*>(d);
     d += sizeof(int) * level_start.size();
     a.roots = reinterpret_cast<const int*>(d);
+    d += sizeof(int) * roots.size();
+    a.wave_root = reinterpret_cast<const int*>(d);
     a.V = V;
     a.n_leaves = (int)leaves.size();
     a.n_inner = (int)inner.size();
