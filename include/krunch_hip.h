@@ -88,10 +88,12 @@ int kr_decode_step_batched(const int32_t* cdfs, int V, const uint8_t* input_buf,
                            int B, int cdf_precision, void* stream);
 
 /* -------------------------------------------------------------------- CDF
- * One 1024-thread workgroup per row; V <= 65536. Probabilities are
+ * One 1024-thread workgroup per row. V <= 65032 or V = 65536: a row is held
+ * in registers as at most 512 leaves of numpy's pairwise summation, and
+ * V in 65033..65535 needs 513 (KR_EUNSUPPORTED). Probabilities are
  * renormalised with numpy's float32 summation order, so results are
  * bit-identical to krunch_ac/cdf.py:22-74. Softmax of fp16 logits (row
- * stride ld elements): e = exp(x - max) with a fixed exp2-based routine,
+ * stride ld elements): e = exp(x - max) with a fixed FMA-based routine,
  * q = e * (1 / sum e), then cdf.py on q.
  */
 
