@@ -77,6 +77,13 @@ struct kr_gemm_multi {
 int kr_gemm_launch(const kr_gemm_args& g, int epilogue, hipStream_t stream);
 // Several products; on the small-M path those sharing M and K run in one
 // launch (independent outputs), otherwise they are launched in order.
+// Width (in 16-column panels) of the column groups the small-M fragment
+// kernel uses for these jobs launched together. When a job has a multiple of 8
+// groups, XCD x takes its groups x, x + 8, ... (workgroups are dealt to the
+// XCDs round robin), so a caller can stage each XCD's weight panels in that
+// XCD's L2 ahead of the launch.
+int kr_gemm_panel_ns(const kr_gemm_args* jobs, int njobs);
+
 int kr_gemm_launch_multi(const kr_gemm_args* jobs, const int* epilogues, int njobs,
                          hipStream_t stream);
 

@@ -771,14 +771,27 @@ long long panel_cost(const kr_gemm_multi& mj, PanelShape sh) {
     return ((wgs + 255) / 256) * per_wg * 4096 - std::min<long long>(wgs, 256);
 }
 
-template <bool FRAG, int MAXT, bool I8, size_t N>
-int launch_best(const kr_gemm_multi& mj, const PanelShape (&shapes)[N], hipStream_t s) {
+template <size_t N>
+PanelShape choose_shape(const kr_gemm_multi& mj, const PanelShape (&shapes)[N]) {
     PanelShape best = shapes[0];
     long long best_cost = panel_cost(mj, best);
     for (size_t i = 1; i < N; i++) {
         const long long c = panel_cost(mj, shapes[i]);
         if (c < best_cost) { best_cost = c; best = shapes[i]; }
     }
+    return best;
+}
+
+PanelShape choose_small_shape(const kr_gemm_multi& mj) {
+    const int S = mj.job[0].K / kKS;
+    if (S <= 4) return choose_shape(mj, kShapes256);
+    if (S <= 12) return choose_shape(mj, kShapes768);
+    return choose_shape(mj, kShapes1024);
+}
+
+template <bool FRAG, int MAXT, bool I8, size_t N>
+int launch_best(const kr_gemm_multi& mj, const PanelShape (&shapes)[N], hipStream_t s) {
+    const PanelShape best = choose_shape(mj, shapes);
 #define KR_PANEL(TM_, NS_) \
     if (best.TM == TM_ && best.NS == NS_) return launch_panel<TM_, NS_, FRAG, MAXT, I8>(mj, s);
     if constexpr (MAXT == 256) {
@@ -856,6 +869,14 @@ int check_args(const kr_gemm_args& g, int ep) {
     KR_REQUIRE((ep != KR_EP_RESID && ep != KR_EP_GATED) || g.res, "gemm: residual missing");
     KR_REQUIRE(ep != KR_EP_GATED || g.gate, "gemm: gate missing");
     return KR_OK;
+}
+
+int kr_gemm_panel_ns(const kr_gemm_args* jobs, int njobs) {
+    if (njobs < 1 || njobs > KR_GEMM_MAX_JOBS || jobs[0].K < kKS || jobs[0].K / kKS > 16) return 0;
+    kr_gemm_multi mj{};
+    mj.njobs = njobs;
+    for (int j = 0; j < njobs; j++) mj.job[j] = jobs[j];
+    return choose_small_shape(mj).NS;
 }
 
 int kr_gemm_launch_multi(const kr_gemm_args* jobs, const int* eps, int njobs, hipStream_t s) {

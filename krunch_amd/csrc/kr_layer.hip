@@ -169,6 +169,19 @@ __device__ __forceinline__ void store_mix_q8(int8_t* __restrict__ out, float* __
     if (lane == 0) scales[row] = s;
 }
 
+// Weight panels to pull into each XCD's L2 while a latency-bound LN-mix runs:
+// region r holds n_groups column groups of group_bytes each (fragment-packed
+// weights, one group per workgroup column group of the product that follows);
+// the extra workgroups of XCD x read groups x, x + 8, ..., the ones that XCD's
+// workgroups will multiply by.
+struct PrefetchSet {
+    const char* base[4];
+    long long group_bytes[4];
+    int n_groups[4];
+    int n;                     // regions
+    int blocks;                // extra workgroups (a multiple of 8)
+};
+
 struct LnMixArgs {
     const kr_half* x;          // [B*T, C]
     const kr_half* ln_w;
@@ -187,7 +200,44 @@ struct LnMixArgs {
     const kr_half* emb;
     int V;
     kr_half* xw;
+    PrefetchSet pf;            // optional L2 staging of the next products' weights
+    int ln_blocks;             // workgroups doing LN-mix rows (set by the launcher)
 };
+
+// The loads only need to reach L2: their values are folded into one register
+// the compiler must keep, and nothing is stored. The 16-byte chunks XCD x
+// stages (all regions, groups x, x + 8, ...) are numbered in one sequence and
+// dealt over the XCD's staging threads, eight loads in flight per thread, so a
+// thread waits on memory about twice rather than once per group.
+__device__ void prefetch_panels(const PrefetchSet& pf, int p) {
+    const int x = p & 7, nr = pf.blocks >> 3;
+    const int t = (p >> 3) * 256 + (int)threadIdx.x, T = nr * 256;
+    int per[4], cum[5];
+    cum[0] = 0;
+    #pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int groups_x = i < pf.n ? (pf.n_groups[i] - x + 7) / 8 : 0;   // groups x, x+8, ...
+        per[i] = i < pf.n ? (int)(pf.group_bytes[i] >> 4) : 1;             // chunks per group
+        cum[i + 1] = cum[i] + groups_x * per[i];
+    }
+    unsigned acc = 0;
+    for (int c0 = t; c0 < cum[4]; c0 += 8 * T) {
+        uint4 v[8];
+        #pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const int c = c0 + u * T;
+            v[u] = make_uint4(0, 0, 0, 0);
+            if (c < cum[4]) {
+                const int i = c < cum[1] ? 0 : (c < cum[2] ? 1 : (c < cum[3] ? 2 : 3));
+                const int r = c - cum[i], gi = r / per[i], o = r - gi * per[i];
+                v[u] = reinterpret_cast<const uint4*>(pf.base[i] + (long long)(x + 8 * gi) * pf.group_bytes[i])[o];
+            }
+        }
+        #pragma unroll
+        for (int u = 0; u < 8; u++) acc ^= v[u].x;
+    }
+    asm volatile("" :: "v"(acc));
+}
 
 // One wave per run of `run` consecutive tokens of one stream. The wave that
 // owns t = 0 reads the carried state first and rewrites it last (with the
@@ -199,6 +249,10 @@ template <int G, int NMIX>
 __global__ void __launch_bounds__(256) ln_mix_kernel(LnMixArgs a) {
     constexpr int C = 256 * G;
     constexpr int NM = NMIX > 0 ? NMIX : 1;
+    if ((int)blockIdx.x >= a.ln_blocks) {   // staging workgroups (uniform per workgroup)
+        prefetch_panels(a.pf, (int)blockIdx.x - a.ln_blocks);
+        return;
+    }
     const int lane = threadIdx.x & 63;
     const int gw = (blockIdx.x * blockDim.x + threadIdx.x) >> 6;
     const int runs = (a.T + a.run - 1) / a.run;
@@ -515,11 +569,16 @@ inline const kr_half* H(const void* p) { return reinterpret_cast<const kr_half*>
 inline kr_half* Hm(void* p) { return reinterpret_cast<kr_half*>(p); }
 
 template <int NMIX>
-int launch_ln_mix(int G, const LnMixArgs& a, hipStream_t s) {
+int launch_ln_mix(int G, const LnMixArgs& a_in, hipStream_t s) {
+    LnMixArgs a = a_in;
     const int runs = (a.T + a.run - 1) / a.run;
     const long long waves = (long long)a.B * runs;
-    const int blocks = (int)((waves + 3) / 4);
-    if (blocks == 0) return KR_OK;
+    if (waves == 0) return KR_OK;
+    // LN-mix workgroups rounded to a multiple of 8 so the staging ones that
+    // follow keep blockIdx % 8 == XCD (the spare LN-mix ones exit at once)
+    a.ln_blocks = (int)((waves + 3) / 4 + 7) / 8 * 8;
+    if (a.pf.n == 0) a.pf.blocks = 0;
+    const int blocks = a.ln_blocks + a.pf.blocks;
     switch (G) {
         case 1: ln_mix_kernel<1, NMIX><<<blocks, 256, 0, s>>>(a); break;
         case 2: ln_mix_kernel<2, NMIX><<<blocks, 256, 0, s>>>(a); break;
@@ -543,18 +602,25 @@ int launch_kvr_wkv_shape(const KvrWkvArgs& a, hipStream_t s) {
     return KR_OK;
 }
 
-template <int S>
-int launch_kvr_wkv_s(const KvrWkvArgs& a, hipStream_t s) {
-    const int shapes[4][2] = {{2, 2}, {2, 1}, {1, 2}, {1, 1}};
+constexpr int kKvrShapes[4][2] = {{2, 2}, {2, 1}, {1, 2}, {1, 1}};   // (TM, NS)
+
+// Shape of the K/V/R + WKV launch for M rows and C = 256 S channels (index
+// into kKvrShapes): busiest-CU line model, ties to more workgroups.
+int kvr_wkv_shape(int S, int M) {
     long long best = -1;
     int bi = 0;
     for (int i = 0; i < 4; i++) {
-        const int TM = shapes[i][0], NS = shapes[i][1];
-        const long long wgs = (long long)((a.M + 16 * TM - 1) / (16 * TM)) * (256 * S / (16 * NS));
+        const int TM = kKvrShapes[i][0], NS = kKvrShapes[i][1];
+        const long long wgs = (long long)((M + 16 * TM - 1) / (16 * TM)) * (256 * S / (16 * NS));
         const long long cost = ((wgs + 255) / 256) * (TM + NS) * 4096 - std::min(wgs, 256ll);
         if (best < 0 || cost < best) { best = cost; bi = i; }
     }
-    switch (bi) {
+    return bi;
+}
+
+template <int S>
+int launch_kvr_wkv_s(const KvrWkvArgs& a, hipStream_t s) {
+    switch (kvr_wkv_shape(S, a.M)) {
         case 0: return launch_kvr_wkv_shape<S, 2, 2>(a, s);
         case 1: return launch_kvr_wkv_shape<S, 2, 1>(a, s);
         case 2: return launch_kvr_wkv_shape<S, 1, 2>(a, s);
@@ -739,10 +805,44 @@ int layer_forward_q8(const kr_layer_weights& L, int C, int F, kr_half* x, int B,
 // Stepped (T = 1) fp16 layer with fragment-packed weights: LN1-mix, the
 // K, V, R products fused with WKV, the output projection, LN2-mix and the
 // channel mix (six launches).
+// Add the fragment-packed weight Wf ([N rows padded to 16] x K) to a staging
+// set, cut into the column groups of NS 16-column panels that the product
+// reading it will use; only when the groups are dealt to XCDs in eights.
+void stage_weight(PrefetchSet& pf, const void* Wf, int N, int K, int NS) {
+    // whole groups only (the buffer ends at the last one), dealt in eights
+    if (!Wf || NS <= 0 || pf.n >= 4 || N % (16 * NS) != 0 || (N / (16 * NS)) % 8 != 0) return;
+    const int groups = N / (16 * NS);
+    pf.base[pf.n] = static_cast<const char*>(Wf);
+    pf.group_bytes[pf.n] = (long long)NS * (K / 32) * 1024;
+    pf.n_groups[pf.n] = groups;
+    pf.n++;
+}
+
+constexpr int kStageBlocks = 512;   // staging workgroups per LN-mix launch (64 per XCD)
+
 int layer_step_fused(const kr_layer_weights& L, int C, int F, kr_half* x, int B,
                      const kr_layer_state& st, const Work& w, hipStream_t s,
                      const EmbedSrc* e) {
     const int M = B, G = C / 256;
+    // Weights the next products read, staged into their XCDs' L2 by the
+    // LN-mix launches (which wait on memory latency, not bandwidth): LN1 stages
+    // K, V, R and the output projection, LN2 the channel-mix value product.
+    // Staging bytes still cost HBM time inside the LN-mix launch; staging the
+    // channel-mix R/K weights too (another 5.9 MB) lengthened LN2 by more than
+    // it saved, measured on MI355X at B = 256.
+    PrefetchSet pf_att{}, pf_ffn{};
+    {
+        const int ns_kvr = kKvrShapes[kvr_wkv_shape(G, M)][1];
+        stage_weight(pf_att, L.Kf, C, C, ns_kvr);
+        stage_weight(pf_att, L.Vf, C, C, ns_kvr);
+        stage_weight(pf_att, L.Rf, C, C, ns_kvr);
+        const kr_gemm_args o = gemm_args(w.ry, M, C, L.Ot, C, x, x, nullptr, L.Of, true);
+        stage_weight(pf_att, L.Of, C, C, kr_gemm_panel_ns(&o, 1));
+        pf_att.blocks = kStageBlocks;
+        const kr_gemm_args v = gemm_args(w.kf, M, F, L.fVt, C, x, x, w.rf, L.fVf, true);
+        stage_weight(pf_ffn, L.fVf, C, F, kr_gemm_panel_ns(&v, 1));
+        pf_ffn.blocks = kStageBlocks;
+    }
     LnMixArgs a{};
     a.x = x;
     a.ln_w = H(L.ln1_w);
@@ -755,6 +855,7 @@ int layer_step_fused(const kr_layer_weights& L, int C, int F, kr_half* x, int B,
     a.run = 1;
     a.frag = 1;
     set_embed(a, e, x);
+    a.pf = pf_att;
     KR_TRY(launch_ln_mix<3>(G, a, s));
     set_embed(a, nullptr, x);
     KvrWkvArgs kw{};
@@ -774,6 +875,7 @@ int layer_step_fused(const kr_layer_weights& L, int C, int F, kr_half* x, int B,
     a.tm[0] = H(L.ftm_k); a.tm[1] = H(L.ftm_r);
     a.out[0] = w.fkx; a.out[1] = w.frx;
     a.state = Hm(st.ffn_xx);
+    a.pf = pf_ffn;
     KR_TRY(launch_ln_mix<2>(G, a, s));
     {
         const kr_gemm_args jobs[2] = {
