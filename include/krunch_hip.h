@@ -226,6 +226,9 @@ typedef struct kr_model_weights {
     const void *ln_out_w, *ln_out_b;      /* fp16 [C] */
     const void* headT;                    /* fp16 [V, C] */
     const kr_layer_weights* layers;       /* host array, n_layer entries */
+    /* Fragment-packed copy of headT (kr_pack_fragments), read by the decode
+     * head (M <= 256 rows, C <= 768); NULL = the row-major head. */
+    const void* headF;
 } kr_model_weights;
 
 /* w = -exp(raw) for the WKV decay (the rwkv loader's transform the reference

@@ -36,7 +36,7 @@ class KrLayerWeights(ctypes.Structure):
 class KrModelWeights(ctypes.Structure):
     _fields_ = [("n_layer", I), ("C", I), ("F", I), ("V", I), ("emb", P),
                 ("ln_out_w", P), ("ln_out_b", P), ("headT", P),
-                ("layers", ctypes.POINTER(KrLayerWeights))]
+                ("layers", ctypes.POINTER(KrLayerWeights)), ("headF", P)]
 
 
 # name -> (argtypes, restype); every int-returning entry point is checked.

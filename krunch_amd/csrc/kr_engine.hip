@@ -23,8 +23,9 @@ int kr_impl_forward_layers_view(const kr_model_weights* m, void* x, int B, int T
                                 int state_B, int b0, void* ws, size_t ws_bytes, hipStream_t s,
                                 const int32_t* ids);
 int kr_impl_embed(const kr_model_weights* m, const int32_t* ids, int M, void* x, hipStream_t s);
+// xn_rows16: xn holds M rounded up to 16 rows (allows the small-M head).
 int kr_impl_head(const kr_model_weights* m, const void* x, int M, void* xn, void* logits,
-                 long long ld, hipStream_t s);
+                 long long ld, hipStream_t s, bool xn_rows16);
 size_t kr_impl_work_bytes(long long M, int C, int F);
 void* kr_impl_head_scratch(void* ws, long long M, int C, int F);
 
@@ -92,7 +93,7 @@ int decode_step(const DecodeStepArgs& a, hipStream_t s) {
     KR_TRY(kr_impl_forward_layers_view(a.m, a.x, a.B, 1, a.state, a.state_B, a.b0, a.ws,
                                        a.ws_bytes, s, a.syms));
     void* xn = kr_impl_head_scratch(a.ws, a.B, a.m->C, a.m->F);
-    KR_TRY(kr_impl_head(a.m, a.x, a.B, xn, a.logits, a.ld, s));
+    KR_TRY(kr_impl_head(a.m, a.x, a.B, xn, a.logits, a.ld, s, true));
     return kr_softmax_cdf_decode(reinterpret_cast<const uint16_t*>(a.logits), a.B, a.m->V, a.ld,
                                  a.in, a.in_len, a.base, a.limits, a.ac_states, a.syms, a.tokens,
                                  a.tok_stride, a.tok_count, a.n_tokens, a.prec, s);
@@ -133,7 +134,7 @@ int kr_embed(const kr_model_weights* m, const int32_t* ids, int M, void* x, void
 int kr_head_logits(const kr_model_weights* m, const void* x, int M, void* xn, void* logits,
                    long long ld, void* stream) {
     KR_REQUIRE(m && x && xn && logits && M >= 0 && ld >= m->V, "kr_head_logits: bad args");
-    return kr_impl_head(m, x, M, xn, logits, ld, kr_stream(stream));
+    return kr_impl_head(m, x, M, xn, logits, ld, kr_stream(stream), M % 16 == 0);
 }
 
 int kr_compress_window(const kr_model_weights* m, const int32_t* inputs, const int32_t* targets,
@@ -152,7 +153,7 @@ int kr_compress_window(const kr_model_weights* m, const int32_t* inputs, const i
         const int n = (int)((M - r0) < head_rows ? (M - r0) : head_rows);
         const void* xr = static_cast<const char*>(x) + (size_t)r0 * m->C * 2;
         void* xnr = static_cast<char*>(xn) + (size_t)r0 * m->C * 2;
-        KR_TRY(kr_impl_head(m, xr, n, xnr, logits, ld, s));
+        KR_TRY(kr_impl_head(m, xr, n, xnr, logits, ld, s, head_rows % 16 == 0));
         KR_TRY(kr_softmax_cdf_pairs(reinterpret_cast<const uint16_t*>(logits), n, m->V, ld,
                                     targets + r0, pairs + 2 * r0, cdf_precision, stream));
     }

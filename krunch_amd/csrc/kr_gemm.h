@@ -87,6 +87,14 @@ int kr_gemm_panel_ns(const kr_gemm_args* jobs, int njobs);
 int kr_gemm_launch_multi(const kr_gemm_args* jobs, const int* epilogues, int njobs,
                          hipStream_t stream);
 
+// out[M, N] (row stride ldo) = fp16(A @ W) for the small-M head (M <= 256,
+// K in {256, 512, 768}): A fragment-packed [M rows padded to 16, K], W^T
+// fragment-packed [N padded to 16, K]. Same contract and bits as
+// kr_gemm_launch with KR_EP_F16.
+bool kr_gemm_head_small_ok(int M, int N, int K);
+int kr_gemm_head_small(const kr_half* Af, const kr_half* Wf, int M, int N, int K, kr_half* out,
+                       long long ldo, hipStream_t stream);
+
 
 // Per-row symmetric int8 quantisation of an fp16 [M, K] matrix (kr_quant.hip).
 int kr_impl_quantize_rows(const void* x, long long ldx, int M, int K, void* q, float* scales,

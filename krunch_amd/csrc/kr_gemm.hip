@@ -813,6 +813,126 @@ int launch_small(const kr_gemm_multi& mj, hipStream_t s) {
     return launch_best<FRAG, 1024, I8>(mj, kShapes1024, s);
 }
 
+// ---------------------------------------------------------------------------
+// Small-M head (the decode step: M <= 256 rows x V = 50277 columns, K = C):
+// the A operand stays in registers for the whole launch and each workgroup
+// streams its own contiguous run of 16-column weight blocks exactly once.
+//
+// The persistent 256x128 kernel re-reads all M rows of A for every
+// 128-column tile: 393 tiles at V = 50277 over 256 CUs, 9,216 L2 lines on the
+// busiest CU. Here wave w holds row blocks 2w, 2w + 1 of the fragment-packed
+// A (2 x K/32 fragments, 8 K/32 VGPRs), so a CU reads A once plus its share
+// of the weights (~5,400 lines). A weight block (16 columns x K, contiguous
+// in the fragment layout) goes into an LDS ring of kHeadStages stages by
+// asynchronous copies issued kHeadStages - 1 blocks ahead; all eight waves
+// multiply each block with their rows.
+// Same reduction contract as every GEMM here (v_mfma_f32_16x16x32_f16 chains
+// over 256-wide slices from zero, added in slice order; MFMA issued as
+// W^T x A^T), then the fp16 epilogue: out = fp16(acc).
+constexpr int kHeadStages = 4;
+#ifndef KR_HEAD_RBW
+#define KR_HEAD_RBW 4
+#endif
+
+// RBW row blocks (16 rows) per wave, 16 / RBW waves: 256 rows per workgroup.
+template <int KB, int RBW>   // KB = K / 32 fragments per row: K = 256, 512 or 768
+__global__ void __launch_bounds__(1024 / RBW, 1) gemm_head_small_kernel(
+        const kr_half* __restrict__ Af, const kr_half* __restrict__ Wf, kr_half* __restrict__ out,
+        long long ldo, int M, int N, int vec) {
+    constexpr int NW = 16 / RBW;     // waves
+    constexpr int CPW = KB / NW;     // 1 KB copies per wave per block
+    constexpr int S = KB / 8;        // 256-wide K slices
+    constexpr int AHEAD = (kHeadStages - 2) * CPW;
+    static_assert(KB % NW == 0 && AHEAD <= 24, "copy split");
+    __shared__ __attribute__((aligned(1024))) kr_half8 ring[kHeadStages * KB * 64];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+    const int nb_total = (N + 15) >> 4;
+    const int b0 = (int)(((long long)blockIdx.x * nb_total) / gridDim.x);
+    const int b1 = (int)(((long long)(blockIdx.x + 1) * nb_total) / gridDim.x);
+    const int nblk = b1 - b0;
+    // this wave's rows (row blocks past the last one re-read it; never stored)
+    const int last_mb = (M - 1) >> 4;
+    const int mb0 = RBW * wave;
+    const bool active = mb0 <= last_mb;
+    kr_half8 a[RBW][KB];
+    if (active) {
+        #pragma unroll
+        for (int i = 0; i < RBW; i++) {
+            const size_t blk = (size_t)min(mb0 + i, last_mb) * KB;
+            #pragma unroll
+            for (int q = 0; q < KB; q++)
+                a[i][q] = *reinterpret_cast<const kr_half8*>(Af + (blk + q) * 512 + lane * 8);
+        }
+    }
+    const unsigned ring_base = (unsigned)(uintptr_t)(__attribute__((address_space(3))) char*)ring;
+    // weight block b0 + j -> stage j % kHeadStages; wave w copies fragments CPW w ..
+    auto issue = [&](int j) {
+        const char* src = reinterpret_cast<const char*>(
+            Wf + ((size_t)(b0 + j) * KB + (size_t)wave * CPW) * 512 + lane * 8);
+        const unsigned dst = ring_base + (unsigned)(((j % kHeadStages) * KB + wave * CPW) * 1024);
+        #pragma unroll
+        for (int u = 0; u < CPW; u++) big_copy(src + u * 1024, dst + u * 1024);
+    };
+    #pragma unroll
+    for (int j = 0; j < kHeadStages - 1; j++)
+        if (j < nblk) issue(j);
+    for (int j = 0; j < nblk; j++) {
+        // the copies of blocks j + 1 .. j + kHeadStages - 2 may stay in flight
+        // (later stores only make the wait stricter: operations retire in
+        // order); near the end everything is waited for
+        if (j + kHeadStages - 2 < nblk) {
+            if constexpr (AHEAD == 24) asm volatile("s_waitcnt vmcnt(24)" ::: "memory");
+            else if constexpr (AHEAD == 16) asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
+            else if constexpr (AHEAD == 12) asm volatile("s_waitcnt vmcnt(12)" ::: "memory");
+            else if constexpr (AHEAD == 8) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+            else if constexpr (AHEAD == 6) asm volatile("s_waitcnt vmcnt(6)" ::: "memory");
+            else if constexpr (AHEAD == 4) asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+            else asm volatile("s_waitcnt vmcnt(2)" ::: "memory");
+        } else {
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        }
+        __syncthreads();   // every wave's copies of block j are in; block j - 1's stage is free
+        if (j + kHeadStages - 1 < nblk) issue(j + kHeadStages - 1);
+        if (!active) continue;
+        const kr_half8* st = ring + (j % kHeadStages) * KB * 64;
+        kr_float4 tot[RBW];
+        #pragma unroll
+        for (int sl = 0; sl < S; sl++) {
+            kr_float4 p[RBW];
+            #pragma unroll
+            for (int i = 0; i < RBW; i++) p[i] = kr_float4{0, 0, 0, 0};
+            #pragma unroll
+            for (int q = 8 * sl; q < 8 * sl + 8; q++) {
+                const kr_half8 w = st[q * 64 + lane];
+                #pragma unroll
+                for (int i = 0; i < RBW; i++)
+                    p[i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(w, a[i][q], p[i], 0, 0, 0);
+            }
+            #pragma unroll
+            for (int i = 0; i < RBW; i++) tot[i] = sl == 0 ? p[i] : add4(tot[i], p[i]);
+        }
+        // lane: row 16 (mb0 + i) + lane % 16, columns n .. n + 3
+        const int n = 16 * (b0 + j) + 4 * (lane >> 4);
+        #pragma unroll
+        for (int i = 0; i < RBW; i++) {
+            const int m = 16 * (mb0 + i) + (lane & 15);
+            if (m >= M) continue;
+            kr_half* dst = out + (size_t)m * (size_t)ldo + n;
+            if (vec && n + 3 < N) {
+                kr_half4 h;
+                #pragma unroll
+                for (int r = 0; r < 4; r++) h[r] = kr_f16(tot[i][r]);
+                *reinterpret_cast<kr_half4*>(dst) = h;
+            } else {
+                #pragma unroll
+                for (int r = 0; r < 4; r++)
+                    if (n + r < N) dst[r] = kr_f16(tot[i][r]);
+            }
+        }
+    }
+}
+
 // Pack Wt [N, K] (row stride ld) into the fragment layout; rows N..N16-1 are zero.
 __global__ void pack_frag_kernel(const kr_half* __restrict__ Wt, long long ld, int N, int K,
                                  kr_half* __restrict__ out) {
@@ -846,6 +966,30 @@ __global__ void transpose_kernel(const kr_half* __restrict__ W, long long ldw_in
 
 
 }  // namespace
+
+bool kr_gemm_head_small_ok(int M, int N, int K) {
+    return M >= 1 && M <= 256 && N >= 1 && (K == 256 || K == 512 || K == 768);
+}
+
+int kr_gemm_head_small(const kr_half* Af, const kr_half* Wf, int M, int N, int K, kr_half* out,
+                       long long ldo, hipStream_t s) {
+    KR_REQUIRE(Af && Wf && out, "head: null pointer");
+    KR_REQUIRE(kr_gemm_head_small_ok(M, N, K), "head: unsupported M=%d N=%d K=%d", M, N, K);
+    KR_REQUIRE(ldo >= N, "head: ldo %lld < N %d", ldo, N);
+    KR_REQUIRE(((uintptr_t)Af & 15) == 0 && ((uintptr_t)Wf & 15) == 0,
+               "head: operands must be 16-byte aligned");
+    const int vec = (ldo & 3) == 0 && ((uintptr_t)out & 7) == 0;
+    const int nb = (N + 15) / 16;
+    const int grid = nb < 256 ? nb : 256;
+    constexpr int R = KR_HEAD_RBW;
+    switch (K) {
+        case 256: gemm_head_small_kernel<8, R><<<grid, 1024 / R, 0, s>>>(Af, Wf, out, ldo, M, N, vec); break;
+        case 512: gemm_head_small_kernel<16, R><<<grid, 1024 / R, 0, s>>>(Af, Wf, out, ldo, M, N, vec); break;
+        default: gemm_head_small_kernel<24, R><<<grid, 1024 / R, 0, s>>>(Af, Wf, out, ldo, M, N, vec); break;
+    }
+    KR_LAUNCHED();
+    return KR_OK;
+}
 
 int check_args(const kr_gemm_args& g, int ep) {
     KR_REQUIRE(g.A && (g.Wt || g.Wf) && g.out, "gemm: null pointer");

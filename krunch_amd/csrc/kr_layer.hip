@@ -112,6 +112,21 @@ __device__ __forceinline__ void store_row(kr_half* __restrict__ p, int lane, con
     }
 }
 
+// Row `row` of a fragment-packed [*, C] operand (kr_frag_index): the lane's
+// 4-column groups are 4 consecutive halves there too.
+template <int G>
+__device__ __forceinline__ void store_row_frag(kr_half* __restrict__ out, size_t row, int lane,
+                                               const RowF<G>& r) {
+    constexpr int C = 256 * G;
+    #pragma unroll
+    for (int i = 0; i < G; i++) {
+        kr_half4 h;
+        #pragma unroll
+        for (int q = 0; q < 4; q++) h[q] = kr_f16(r.v[i][q]);
+        *reinterpret_cast<kr_half4*>(out + kr_frag_index((long long)row, 256 * i + 4 * lane, C)) = h;
+    }
+}
+
 // mix = fp16(xx * tm + sx * (1 - tm))   (premix_kernels.cu:19-54 semantics),
 // stored into row `row` of a row-major or fragment-packed [*, C] operand.
 template <int G>
@@ -291,7 +306,8 @@ __global__ void __launch_bounds__(256) ln_mix_kernel(LnMixArgs a) {
         to_float<G>(first_h, cur);
         layer_norm_row<G>(cur, w, bias);
         if constexpr (NMIX == 0) {
-            store_row<G>(a.out[0] + (row0 + t) * C, lane, cur);
+            if (a.frag) store_row_frag<G>(a.out[0], row0 + t, lane, cur);
+            else store_row<G>(a.out[0] + (row0 + t) * C, lane, cur);
         } else {
             #pragma unroll
             for (int m = 0; m < NMIX; m++) {
@@ -1026,9 +1042,13 @@ int kr_impl_embed(const kr_model_weights* m, const int32_t* ids, int M, void* x,
 }
 
 // logits[M, ld] = fp16(LN_out(x) @ head); xn is an [M, C] fp16 scratch.
+// Up to 256 rows (the decode step) with a fragment-packed head: LN_out writes
+// xn fragment-packed and the small-M head kernel reads it (same bits). That
+// needs xn to hold M rounded up to 16 rows (xn_rows16).
 int kr_impl_head(const kr_model_weights* m, const void* x, int M, void* xn, void* logits,
-                 long long ld, hipStream_t s) {
+                 long long ld, hipStream_t s, bool xn_rows16) {
     if (M == 0) return KR_OK;
+    const bool small = xn_rows16 && m->headF && kr_gemm_head_small_ok(M, m->V, m->C);
     LnMixArgs a{};
     a.x = H(x);
     a.ln_w = H(m->ln_out_w);
@@ -1037,7 +1057,10 @@ int kr_impl_head(const kr_model_weights* m, const void* x, int M, void* xn, void
     a.B = M;
     a.T = 1;
     a.run = 1;
+    a.frag = small ? 1 : 0;
     KR_TRY(launch_ln_mix<0>(m->C / 256, a, s));
+    if (small)
+        return kr_gemm_head_small(H(xn), H(m->headF), M, m->V, m->C, Hm(logits), ld, s);
     kr_gemm_args g{};
     g.A = H(xn);
     g.lda = m->C;

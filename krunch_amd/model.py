@@ -97,6 +97,7 @@ def prepare(w: dict, device=None, w8a8: bool = False) -> Prepared:
     t["emb"] = w["emb.weight"].to(device=device, dtype=torch.float16).contiguous()
     t["ln_out_w"], t["ln_out_b"] = h(w["ln_out.weight"]), h(w["ln_out.bias"])
     t["headT"] = _transposed(w["head.weight"], device)
+    t["headF"] = _fragments(t["headT"])
     layers = (_lib.KrLayerWeights * n_layer)()
     for i in range(n_layer):
         a, f, b = f"blocks.{i}.att.", f"blocks.{i}.ffn.", f"blocks.{i}."
@@ -137,7 +138,8 @@ def prepare(w: dict, device=None, w8a8: bool = False) -> Prepared:
     P.layers_c = layers
     P.model_c = _lib.KrModelWeights(n_layer, C, F, V, t["emb"].data_ptr(), t["ln_out_w"].data_ptr(),
                                     t["ln_out_b"].data_ptr(), t["headT"].data_ptr(),
-                                    ctypes.cast(layers, ctypes.POINTER(_lib.KrLayerWeights)))
+                                    ctypes.cast(layers, ctypes.POINTER(_lib.KrLayerWeights)),
+                                    t["headF"].data_ptr())
     return P
 
 

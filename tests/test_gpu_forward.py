@@ -152,3 +152,30 @@ def test_pack_fragments_layout():
     pad[:N] = Wt
     want = pad.view(3, 16, K // 32, 4, 8).permute(0, 2, 3, 1, 4).reshape(-1)
     assert torch.equal(out, want)
+
+
+@pytest.mark.parametrize("M", [16, 48, 256])
+def test_small_head_equals_tiled_head(model, M):
+    """The decode head (A held in registers, fragment-packed weights streamed
+    once, M <= 256) gives the 256x128 persistent kernel's logits bit for bit,
+    including the 5-column tail block of V = 50277 and a padded row stride."""
+    from krunch_amd import _lib
+    import ctypes
+    _, W = model
+    P = W["prepared"]
+    m_row, _keep = _row_major_only(P)      # no fragment-packed head
+    g = torch.Generator(device="cpu").manual_seed(M)
+    x = torch.randn((M, P.C), generator=g).half().cuda()
+    ld = P.V + 3
+    outs = []
+    for mdesc in (P.model_c, m_row):
+        xn = torch.empty((M, P.C), dtype=torch.float16, device="cuda")
+        logits = torch.full((M, ld), float("nan"), dtype=torch.float16, device="cuda")
+        _lib.call("kr_head_logits", ctypes.byref(mdesc), x.data_ptr(), M, xn.data_ptr(),
+                  logits.data_ptr(), ld, _lib.stream_ptr())
+        outs.append(logits)
+    assert torch.equal(outs[0][:, :P.V], outs[1][:, :P.V])
+    assert torch.isnan(outs[0][:, P.V:]).all()       # padding columns untouched
+    ref = torch.nn.functional.layer_norm(x.float(), (P.C,), eps=1e-5) @ \
+        P.tensors["headT"].float().t()
+    assert (outs[0][:, :P.V].float() - ref).abs().max() < 2e-2
