@@ -217,6 +217,7 @@ struct LnMixArgs {
     kr_half* xw;
     PrefetchSet pf;            // optional L2 staging of the next products' weights
     int ln_blocks;             // workgroups doing LN-mix rows (set by the launcher)
+    int one_row;               // one row per workgroup (wave 0; set by the launcher)
 };
 
 // The loads only need to reach L2: their values are folded into one register
@@ -269,8 +270,9 @@ __global__ void __launch_bounds__(256) ln_mix_kernel(LnMixArgs a) {
         return;
     }
     const int lane = threadIdx.x & 63;
-    const int gw = (blockIdx.x * blockDim.x + threadIdx.x) >> 6;
     const int runs = (a.T + a.run - 1) / a.run;
+    int gw = (blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+    if (a.one_row) gw = threadIdx.x < 64 ? (int)blockIdx.x : a.B * runs;
     if (gw >= a.B * runs) return;
     const int b = gw / runs, t0 = (gw % runs) * a.run;
     const int t1 = min(a.T, t0 + a.run);
@@ -592,7 +594,10 @@ int launch_ln_mix(int G, const LnMixArgs& a_in, hipStream_t s) {
     if (waves == 0) return KR_OK;
     // LN-mix workgroups rounded to a multiple of 8 so the staging ones that
     // follow keep blockIdx % 8 == XCD (the spare LN-mix ones exit at once)
-    a.ln_blocks = (int)((waves + 3) / 4 + 7) / 8 * 8;
+    // T = 1 rows (the decode step): one row per workgroup, spread over the
+    // CUs; otherwise four waves (runs of rows) per workgroup
+    a.one_row = a.T == 1 && waves <= 1024 ? 1 : 0;
+    a.ln_blocks = (int)((a.one_row ? waves : (waves + 3) / 4) + 7) / 8 * 8;
     if (a.pf.n == 0) a.pf.blocks = 0;
     const int blocks = a.ln_blocks + a.pf.blocks;
     switch (G) {
