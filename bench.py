@@ -91,7 +91,14 @@ def kernel_probe(weights16, B):
                   att_xx.data_ptr(), aa0.data_ptr(), bb0.data_ptr(), pp0.data_ptr(),
                   ffn_xx.data_ptr(), ws.data_ptr(), nbytes, s)
     torch.cuda.synchronize()
-    del ws
+    # the decode head at B rows (LN_out, then the small-M head kernel)
+    xn = torch.empty((B, P.C), dtype=torch.float16, device=dev)   # B % 16 == 0 at the bench shapes
+    ld = cpp_path.logits_ld(P.V)
+    hl = torch.empty((B, ld), dtype=torch.float16, device=dev)
+    for _ in range(2):
+        _lib.call("kr_head_logits", P.ptr, x.data_ptr(), B, xn.data_ptr(), hl.data_ptr(), ld, s)
+    torch.cuda.synchronize()
+    del ws, xn, hl
     # packed channel-mix value product at the window shape (B * 1024 rows) on the large-M kernel
     Mp = B * 1024
     A = torch.rand((Mp, K), device=dev).half()
