@@ -401,6 +401,9 @@ __global__ void __launch_bounds__(512, 1) gemm_big_kernel(kr_gemm_args g, int n_
                 for (int i = 0; i < 4; i++) a[i] = As[big_pos(64 * wm + 16 * i + lr, 4 * kb + lq)];
                 #pragma unroll
                 for (int t = 0; t < 4; t++) w[t] = Ws[big_pos(64 * wn + 16 * t + lr, 4 * kb + lq)];
+                // all eight fragment reads before the 16 MFMAs: one LDS wait per
+                // 32-wide block instead of one per row block
+                __builtin_amdgcn_sched_barrier(0);
                 #pragma unroll
                 for (int i = 0; i < 4; i++)
                     #pragma unroll
@@ -903,12 +906,16 @@ __global__ void __launch_bounds__(1024 / RBW, 1) gemm_head_small_kernel(
             kr_float4 p[RBW];
             #pragma unroll
             for (int i = 0; i < RBW; i++) p[i] = kr_float4{0, 0, 0, 0};
+            // the slice's 8 weight fragments read before its MFMAs (one LDS wait)
+            kr_half8 w[8];
             #pragma unroll
-            for (int q = 8 * sl; q < 8 * sl + 8; q++) {
-                const kr_half8 w = st[q * 64 + lane];
+            for (int q = 0; q < 8; q++) w[q] = st[(8 * sl + q) * 64 + lane];
+            __builtin_amdgcn_sched_barrier(0);
+            #pragma unroll
+            for (int q = 0; q < 8; q++) {
                 #pragma unroll
                 for (int i = 0; i < RBW; i++)
-                    p[i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(w, a[i][q], p[i], 0, 0, 0);
+                    p[i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(w[q], a[i][8 * sl + q], p[i], 0, 0, 0);
             }
             #pragma unroll
             for (int i = 0; i < RBW; i++) tot[i] = sl == 0 ? p[i] : add4(tot[i], p[i]);
