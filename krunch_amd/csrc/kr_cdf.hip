@@ -124,20 +124,71 @@ __device__ __forceinline__ float load_val(const void* row, const kr_half* stage,
     else return reinterpret_cast<const float*>(row)[i];
 }
 
+// A row's values in flight to the stage: every load of the row is issued
+// before any is written (V <= 65536 is at most 8 chunks of 8 per thread), so
+// staging costs one memory round trip, not one per chunk.
+constexpr int kStageChunks = 8;
+struct StagedRow {
+    kr_half8 c[kStageChunks];
+    kr_half h0, h1;   // this thread's element of the unaligned head / of the tail
+};
+
+// Load V fp16 values at rp (2-byte aligned) for the stage (see StageMap).
+__device__ __forceinline__ StageMap stage_row_load(const kr_half* __restrict__ rp, int V, int tid,
+                                                   StagedRow& r) {
+    const int head = min((int)(((16 - ((uintptr_t)rp & 15)) & 15) >> 1), V);
+    const int pad = (8 - head) & 7;
+    const int nchunks = (V - head) / 8;
+    #pragma unroll
+    for (int u = 0; u < kStageChunks; u++) {
+        const int c = tid + u * kThreads;
+        if (c < nchunks) r.c[u] = *reinterpret_cast<const kr_half8*>(rp + head + 8 * c);
+    }
+    const int tail0 = head + 8 * nchunks;
+    if (tid < head) r.h0 = rp[tid];
+    if (tid >= 8 && tid - 8 < V - tail0) r.h1 = rp[tail0 + tid - 8];
+    return StageMap{pad, head};
+}
+
+// Write what stage_row_load loaded into the stage.
+__device__ __forceinline__ void stage_row_store(int V, kr_half* stage, int tid, StageMap sm,
+                                                const StagedRow& r) {
+    const int nchunks = (V - sm.head) / 8;
+    #pragma unroll
+    for (int u = 0; u < kStageChunks; u++) {
+        const int c = tid + u * kThreads;
+        if (c < nchunks)
+            *reinterpret_cast<kr_half8*>(stage + sm.pad + sm.head + 8 * c + ((c >> 4) << 3)) = r.c[u];
+    }
+    const int tail0 = sm.head + 8 * nchunks;
+    if (tid < sm.head) stage[sm.at(tid)] = r.h0;
+    if (tid >= 8 && tid - 8 < V - tail0) stage[sm.at(tail0 + tid - 8)] = r.h1;
+}
+
 // Copy V fp16 values at rp (2-byte aligned) into the stage (see StageMap).
 __device__ __forceinline__ StageMap stage_row(const kr_half* __restrict__ rp, int V, kr_half* stage,
                                               int tid) {
-    const int head = min((int)(((16 - ((uintptr_t)rp & 15)) & 15) >> 1), V);
-    const int pad = (8 - head) & 7;
-    const StageMap sm{pad, head};
-    const int nchunks = (V - head) / 8;
-    for (int c = tid; c < nchunks; c += kThreads)
-        *reinterpret_cast<kr_half8*>(stage + pad + head + 8 * c + ((c >> 4) << 3)) =
-            *reinterpret_cast<const kr_half8*>(rp + head + 8 * c);
-    const int tail0 = head + 8 * nchunks;
-    if (tid < head) stage[sm.at(tid)] = rp[tid];
-    if (tid >= 8 && tid - 8 < V - tail0) stage[sm.at(tail0 + tid - 8)] = rp[tail0 + tid - 8];
+    StagedRow r;
+    const StageMap sm = stage_row_load(rp, V, tid, r);
+    stage_row_store(V, stage, tid, sm, r);
     return sm;
+}
+
+// The summation plan into LDS: all loads issued before the LDS writes.
+__device__ __forceinline__ void copy_plan(const PlanArgs& P, RowShared& sh, int tid) {
+    const bool a = tid < P.n_inner, b = tid <= P.n_levels, c = tid < P.n_blocks,
+               d = tid < kMaxIt * kWaves;
+    int2 vi = make_int2(0, 0);
+    int vl = 0, vr = 0, vw = 0;
+    if (a) vi = P.inner[tid];
+    if (b) vl = P.level_start[tid];
+    if (c) vr = P.roots[tid];
+    if (d) vw = P.wave_root[tid];
+    if (a) sh.inner[tid] = vi;
+    if (b) sh.level_start[tid] = vl;
+    if (c) sh.roots[tid] = vr;
+    if (d) sh.wave_root[tid] = vw;
+    for (int i = tid + kThreads; i < P.n_inner; i += kThreads) sh.inner[i] = P.inner[i];
 }
 
 // a / b correctly rounded (IEEE binary32, round to nearest), given
@@ -299,33 +350,46 @@ __device__ __forceinline__ void cdf_row(const void* __restrict__ input, long lon
     const int grp = lane >> 3, j = lane & 7;
     const int V = P.V;
 
-    // Decoder state and the stream bits this step will consume, fetched by
-    // lane 0 up front so their latency overlaps the softmax.
-    kr_rc_state dst{};
-    kr_bit_window win{};
-    if constexpr (MODE == M_DECODE) {
-        static_assert(IN == IN_LOGITS_F16, "decode reads fp16 logits");
-        // Finished streams do nothing this step (uniform per workgroup).
-        if (D.n_tokens && D.tok_count && D.tok_count[row] >= D.n_tokens[row]) return;
-        if (tid == 0) {
-            dst = D.states[row];
-            const uint32_t o = D.base ? (uint32_t)D.base[row] : 0u;
-            uint32_t lim = D.in_len > o ? D.in_len - o : 0u;
-            if (D.limits && (uint32_t)D.limits[row] < lim) lim = (uint32_t)D.limits[row];
-            win.open(D.in + (o < D.in_len ? o : 0u), lim, dst.bit_offset);
-        }
-    }
-
     const char* rowp;
     if constexpr (IN == IN_LOGITS_F16)
         rowp = reinterpret_cast<const char*>(input) + (size_t)row * (size_t)ld * 2;
     else
         rowp = reinterpret_cast<const char*>(input) + (size_t)row * (size_t)ld * 4;
 
+    // Decode: the decoder state and the stream bits this step will consume
+    // (lane 0), the logits row and the summation plan are all requested
+    // before anything waits, so the prologue costs about two memory round
+    // trips (state, then the bits at its offset). Loads retire in order: the
+    // state goes out first so that waiting for it does not wait for the row.
+    kr_rc_state dst{};
+    kr_bit_window win{};
     StageMap pad{0, 0};
+    if constexpr (MODE == M_DECODE) {
+        static_assert(IN == IN_LOGITS_F16, "decode reads fp16 logits");
+        uint32_t o = 0, lim_cap = 0xFFFFFFFFu;
+        if (tid == 0) {
+            dst = D.states[row];
+            o = D.base ? (uint32_t)D.base[row] : 0u;
+            if (D.limits) lim_cap = (uint32_t)D.limits[row];
+        }
+        StagedRow staged;
+        pad = stage_row_load(reinterpret_cast<const kr_half*>(rowp), V, tid, staged);
+        // Finished streams do nothing this step (uniform per workgroup).
+        if (D.n_tokens && D.tok_count && D.tok_count[row] >= D.n_tokens[row]) return;
+        if (tid == 0) {
+            uint32_t lim = D.in_len > o ? D.in_len - o : 0u;
+            if (lim_cap < lim) lim = lim_cap;
+            win.open(D.in + (o < D.in_len ? o : 0u), lim, dst.bit_offset);
+        }
+        copy_plan(P, sh, tid);
+        stage_row_store(V, stage, tid, pad, staged);
+    }
+
     if constexpr (IN == IN_LOGITS_F16) {
-        if (async_stage) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        else pad = stage_row(reinterpret_cast<const kr_half*>(rowp), V, stage, tid);
+        if constexpr (MODE != M_DECODE) {
+            if (async_stage) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            else pad = stage_row(reinterpret_cast<const kr_half*>(rowp), V, stage, tid);
+        }
         if constexpr (MODE == M_DECODE) {
             if (tid == 0) {   // parked in LDS until the symbol is known
                 sh.dstate = dst;
@@ -707,10 +771,7 @@ row_cdf_kernel(const void* __restrict__ input, long long ld, int n_rows, PlanArg
     __shared__ RowShared sh;
     __shared__ __attribute__((aligned(16))) kr_half stage[IN == IN_LOGITS_F16 ? kStageMax : 8];
     const int tid = threadIdx.x;
-    for (int i = tid; i < P.n_inner; i += kThreads) sh.inner[i] = P.inner[i];
-    if (tid <= P.n_levels) sh.level_start[tid] = P.level_start[tid];
-    if (tid < P.n_blocks) sh.roots[tid] = P.roots[tid];
-    if (tid < kMaxIt * kWaves) sh.wave_root[tid] = P.wave_root[tid];
+    if constexpr (MODE != M_DECODE) copy_plan(P, sh, tid);   // decode copies it after its first loads
     const unsigned stage_lds = (unsigned)(uintptr_t)(__attribute__((address_space(3))) char*)stage;
     if constexpr (MODE == M_PAIRS && IN == IN_LOGITS_F16) {
         const int G = (int)gridDim.x;

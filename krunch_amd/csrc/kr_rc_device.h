@@ -88,12 +88,18 @@ struct kr_bit_window {
         base = bitpos & ~7u;
         const uint32_t byte = bitpos >> 3;
         w = 0;
+        if (limit == 0) return;
+        // eight loads at in-bounds (clamped) addresses, issued together; bytes
+        // past the limit read as zero
+        uint32_t v[8];
         #pragma unroll
         for (int i = 0; i < 8; i++) {
             const uint32_t bi = byte + (uint32_t)i;
-            const uint64_t v = bi < limit ? (uint64_t)buf[bi] : 0ull;
-            w |= v << (56 - 8 * i);
+            v[i] = buf[bi < limit ? bi : limit - 1u];
         }
+        #pragma unroll
+        for (int i = 0; i < 8; i++)
+            if (byte + (uint32_t)i < limit) w |= (uint64_t)v[i] << (56 - 8 * i);
     }
     __device__ uint32_t get() {
         const uint32_t off = pos - base;
