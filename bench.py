@@ -41,6 +41,8 @@ def parse():
     ap.add_argument("--window", type=int, default=1024)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-decode-steps", type=int, default=48)
+    ap.add_argument("--head-rows", type=int, default=4096,
+                    help="compress: rows per head GEMM + CDF block (the logits buffer holds this many rows)")
     ap.add_argument("--groups", type=int, default=1,
                     help="decode the B streams as this many concurrent groups (graph branches)")
     ap.add_argument("--no-w8a8", action="store_true",
@@ -174,7 +176,7 @@ def gpu_bench(args, weights16, w8a8=False):
     M = B * Tw
     ws, ws_bytes = cpp_path.workspace(W, M)
     x = torch.empty((M, P.C), dtype=torch.float16, device=dev)
-    head_rows = min(M, 4096)
+    head_rows = min(M, args.head_rows)
     ld = cpp_path.logits_ld(P.V)
     logits = torch.empty((head_rows, ld), dtype=torch.float16, device=dev)
     # the encoder of window w overlaps the forward of window w+1 (its own

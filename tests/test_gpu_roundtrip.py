@@ -36,6 +36,17 @@ def test_roundtrip_ragged_streams(eng):
         np.testing.assert_array_equal(d, t)
 
 
+@pytest.mark.parametrize("B", [37, 200])
+def test_roundtrip_many_streams(eng, B):
+    """Decode steps of 37 and 200 streams: the decode head's last row block is
+    partial and, at 200, several of its waves hold rows and one holds part."""
+    toks = [synthetic.zipf_tokens(1, 12 + (i % 5), seed_base=1300 + i)[0] for i in range(B)]
+    enc = eng.compress_tokens_batched(toks)
+    dec = eng.decompress_tokens_batched(enc)
+    for t, d in zip(toks, dec):
+        np.testing.assert_array_equal(d, t)
+
+
 def test_decode_groups_and_graph_agree(eng):
     """Concurrent decode groups (graph branches) and the eager path decode the
     same tokens as one group."""
