@@ -41,6 +41,36 @@ BOS_TOKEN = 0
 CDF_PRECISION = 24
 
 
+# Streams per lockstep call (the role of cpp_path.py:531-580
+# compute_decompress_batch, sized for MI355X by measurement rather than by
+# SM count). Decompress at the config-5 window on one MI355X: B = 128, 256,
+# 384, 512 give 1,074, 1,799, 1,857, 2,283 KB/s. 512 rows is the largest batch
+# the fused stepped kernels take (small-M GEMMs, fragment-packed operands),
+# and B x 1024-token windows stay under the forward's 2^31 / F row limit.
+DEFAULT_STREAM_BATCH = 512
+
+
+def _env_batch(name: str, n_chunks: int, default: int) -> int:
+    B = default
+    env = os.environ.get(name)
+    if env:
+        try:
+            B = max(1, int(env))
+        except ValueError:
+            pass
+    return max(1, min(n_chunks, B)) if n_chunks > 0 else B
+
+
+def compute_decompress_batch(n_chunks: int = -1, default: int = DEFAULT_STREAM_BATCH) -> int:
+    """Streams decoded in one lockstep call; $KRUNCH_DECOMPRESS_BATCH overrides."""
+    return _env_batch("KRUNCH_DECOMPRESS_BATCH", n_chunks, default)
+
+
+def compute_compress_batch(n_chunks: int = -1, default: int = DEFAULT_STREAM_BATCH) -> int:
+    """Streams compressed in one packed call; $KRUNCH_COMPRESS_BATCH overrides."""
+    return _env_batch("KRUNCH_COMPRESS_BATCH", n_chunks, default)
+
+
 def encode_header(original_len: int, n_chunks: int, crc32: int, adapter_id: int = 0,
                   adapter_version: int = 0, flags: int = 0, model_id: int = MODEL_ID,
                   tokenizer_id: int = TOKENIZER_ID) -> bytes:
@@ -110,14 +140,22 @@ class InferenceEngine:
     # -------------------------------------------------------------- compress
     def compress_tokens_batched(self, token_streams: Sequence[np.ndarray],
                                 orig_lens: Optional[Sequence[int]] = None) -> List[bytes]:
-        """B token streams -> B chunk payloads (">II" mini-header + bits)."""
+        """B token streams -> B chunk payloads (">II" mini-header + bits), in
+        calls of at most compute_compress_batch() streams."""
         assert self._ready, "call load() first"
-        W = self._weights
-        P = W["prepared"]
-        dev = P.device
         B = len(token_streams)
         if B == 0:
             return []
+        cap = compute_compress_batch(B)
+        if B > cap:
+            res: List[bytes] = []
+            for i in range(0, B, cap):
+                res += self.compress_tokens_batched(
+                    token_streams[i:i + cap], None if orig_lens is None else orig_lens[i:i + cap])
+            return res
+        W = self._weights
+        P = W["prepared"]
+        dev = P.device
         lens = np.array([len(t) for t in token_streams], dtype=np.int64)
         if (lens < 1).any():
             raise ValueError("chunk has no tokens")
@@ -195,14 +233,21 @@ class InferenceEngine:
 
     # ------------------------------------------------------------ decompress
     def decompress_tokens_batched(self, encoded_chunks: Sequence[bytes]) -> List[np.ndarray]:
-        """Chunk payloads -> token streams, B streams decoded in lockstep."""
+        """Chunk payloads -> token streams, decoded in lockstep in calls of at
+        most compute_decompress_batch() streams."""
         assert self._ready, "call load() first"
-        W = self._weights
-        P = W["prepared"]
-        dev = P.device
         B = len(encoded_chunks)
         if B == 0:
             return []
+        cap = compute_decompress_batch(B)
+        if B > cap:
+            res: List[np.ndarray] = []
+            for i in range(0, B, cap):
+                res += self.decompress_tokens_batched(encoded_chunks[i:i + cap])
+            return res
+        W = self._weights
+        P = W["prepared"]
+        dev = P.device
         n_tok, streams = [], []
         for enc in encoded_chunks:
             _, nt = struct.unpack(">II", enc[:8])

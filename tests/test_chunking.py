@@ -57,3 +57,18 @@ def test_truncated_blob():
         chunking.parse_entries(blob[:-1], n)
     with pytest.raises(ValueError):
         chunking.parse_entries(blob, n + 1)
+
+
+def test_stream_batch_sizing(monkeypatch):
+    from krunch_amd import inference as inf
+    monkeypatch.delenv("KRUNCH_DECOMPRESS_BATCH", raising=False)
+    monkeypatch.delenv("KRUNCH_COMPRESS_BATCH", raising=False)
+    assert inf.compute_decompress_batch() == inf.DEFAULT_STREAM_BATCH == 512
+    assert inf.compute_decompress_batch(7) == 7
+    assert inf.compute_compress_batch(5000) == 512
+    monkeypatch.setenv("KRUNCH_DECOMPRESS_BATCH", "3")
+    assert inf.compute_decompress_batch(10) == 3 and inf.compute_decompress_batch(2) == 2
+    monkeypatch.setenv("KRUNCH_DECOMPRESS_BATCH", "junk")
+    assert inf.compute_decompress_batch(1000) == 512
+    monkeypatch.setenv("KRUNCH_COMPRESS_BATCH", "0")
+    assert inf.compute_compress_batch(9) == 1

@@ -47,6 +47,20 @@ def test_roundtrip_many_streams(eng, B):
         np.testing.assert_array_equal(d, t)
 
 
+def test_split_batches_are_byte_identical(eng, monkeypatch):
+    """Jobs larger than the stream batch run as several lockstep calls; every
+    stream's payload and tokens are the same as in one call (streams are
+    independent and every kernel is row-local in its bits)."""
+    toks = [synthetic.zipf_tokens(1, 20 + 9 * i, seed_base=1700 + i)[0] for i in range(7)]
+    whole = eng.compress_tokens_batched(toks)
+    monkeypatch.setenv("KRUNCH_COMPRESS_BATCH", "3")
+    monkeypatch.setenv("KRUNCH_DECOMPRESS_BATCH", "2")
+    split = eng.compress_tokens_batched(toks)
+    assert split == whole
+    for t, d in zip(toks, eng.decompress_tokens_batched(whole)):
+        np.testing.assert_array_equal(d, t)
+
+
 def test_decode_groups_and_graph_agree(eng):
     """Concurrent decode groups (graph branches) and the eager path decode the
     same tokens as one group."""
