@@ -154,11 +154,12 @@ def test_pack_fragments_layout():
     assert torch.equal(out, want)
 
 
-@pytest.mark.parametrize("M", [16, 48, 256])
+@pytest.mark.parametrize("M", [16, 48, 256, 400, 512])
 def test_small_head_equals_tiled_head(model, M):
     """The decode head (A held in registers, fragment-packed weights streamed
-    once, M <= 256) gives the 256x128 persistent kernel's logits bit for bit,
-    including the 5-column tail block of V = 50277 and a padded row stride."""
+    once; 256-row launches up to 512 rows) gives the 256x128 persistent
+    kernel's logits bit for bit, including the 5-column tail block of
+    V = 50277 and a padded row stride."""
     from krunch_amd import _lib
     import ctypes
     _, W = model

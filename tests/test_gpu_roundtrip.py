@@ -36,10 +36,11 @@ def test_roundtrip_ragged_streams(eng):
         np.testing.assert_array_equal(d, t)
 
 
-@pytest.mark.parametrize("B", [37, 200])
+@pytest.mark.parametrize("B", [37, 200, 300])
 def test_roundtrip_many_streams(eng, B):
-    """Decode steps of 37 and 200 streams: the decode head's last row block is
-    partial and, at 200, several of its waves hold rows and one holds part."""
+    """Decode steps of 37, 200 and 300 streams: the decode head's last row
+    block is partial; at 200 several of its waves hold rows and one holds
+    part; at 300 the head runs as a 256-row and a 44-row launch."""
     toks = [synthetic.zipf_tokens(1, 12 + (i % 5), seed_base=1300 + i)[0] for i in range(B)]
     enc = eng.compress_tokens_batched(toks)
     dec = eng.decompress_tokens_batched(enc)
