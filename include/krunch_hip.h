@@ -251,6 +251,22 @@ int kr_layer_step(const kr_layer_weights* L, int C, int F, void* x, int B, int T
                   void* att_xx, float* aa, float* bb, float* pp, void* ffn_xx, void* ws,
                   size_t ws_bytes, void* stream);
 
+/* Layer phase profiler; replaces the reference's KRUNCH_PHASE_PROFILE
+ * profiler with read_phase_times / reset_phase_times (layer_cpp.cpp:111-157,
+ * 825-836). When on, every kr_layer_step call (outside stream capture)
+ * records HIP events between its phases on its stream, waits for the last one
+ * and adds the elapsed milliseconds to running sums. The phases (this build's
+ * kernel split; a fused launch leaves the phase it absorbed empty) are
+ * kr_phase_name(0..kr_phase_count()-1): ln1_mix, kvr_matmul, wkv,
+ * ow_matmul_residual, ln2_mix, ffn_rk_matmul, ffn_v_matmul_residual.
+ * kr_phase_profile(1 / 0) turns it on / off and returns the previous state
+ * (-1 only queries); KRUNCH_PHASE_PROFILE=1 turns it on at first use. */
+int kr_phase_profile(int enable);
+int kr_phase_count(void);
+const char* kr_phase_name(int i);
+int kr_read_phase_times(double* ms, int n, long long* call_count);
+int kr_reset_phase_times(void);
+
 /* replaces launch_krunch_wkv_forward (wkv_kernel.cu:75-92), fused with the
  * receptance: ry = fp16(r * fp16(y)); k, v fp32 [B*T, C], r/ry fp16. */
 int kr_wkv(int B, int T, int C, const float* decay, const float* first, const float* k,

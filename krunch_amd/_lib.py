@@ -72,6 +72,11 @@ _SIGS = {
     "kr_forward_workspace_bytes": ([LL, I, I], SZ),
     "kr_layer_step": ([ctypes.POINTER(KrLayerWeights), I, I, P, I, I, P, P, P, P, P, P, SZ, P], I),
     "kr_wkv": ([I, I, I, P, P, P, P, P, P, P, P, P, P], I),
+    "kr_phase_profile": ([I], I),
+    "kr_phase_count": ([], I),
+    "kr_phase_name": ([I], ctypes.c_char_p),
+    "kr_read_phase_times": ([ctypes.POINTER(ctypes.c_double), I, ctypes.POINTER(LL)], I),
+    "kr_reset_phase_times": ([], I),
     "kr_forward_layers": ([ctypes.POINTER(KrModelWeights), P, I, I, P, P, SZ, P], I),
     "kr_embed": ([ctypes.POINTER(KrModelWeights), P, I, P, P], I),
     "kr_head_logits": ([ctypes.POINTER(KrModelWeights), P, I, P, P, LL, P], I),
@@ -117,6 +122,20 @@ def call(name: str, *args):
         msg = lib().kr_last_error().decode(errors="replace")
         raise KrunchError(f"{name} failed ({rc}): {msg}")
     return rc
+
+
+U32_MAX = 0xFFFFFFFF
+I32_MAX = 0x7FFFFFFF
+
+
+def u32(n: int, what: str = "size") -> int:
+    """A byte count passed as uint32_t: ctypes would truncate silently, so
+    anything outside [0, 2^32) is an error here."""
+    n = int(n)
+    if n < 0 or n > U32_MAX:
+        raise ValueError(f"{what} = {n} does not fit the 32-bit coder interface "
+                         f"(split the call so it stays <= {U32_MAX})")
+    return n
 
 
 def ptr(t) -> int | None:

@@ -3,8 +3,9 @@
 
 Same function names and argument meaning: `init_weights`, `fresh_state`,
 `fresh_state_batched`, `forward_packed`, `forward_packed_window`,
-`forward_stepped`, `forward_stepped_batched`, `softmax_cdfs_per_row`,
-`softmax_cdf_one_row`, `compute_decompress_batch`. Packed and stepped calls
+`forward_stepped`, `forward_stepped_graphed`, `forward_stepped_batched`,
+`softmax_cdfs_per_row`, `softmax_cdf_one_row`, `compute_decompress_batch`,
+`pick_decompress_batch`. Packed and stepped calls
 are bit-identical per row (one GEMM reduction order, shared elementwise
 code), which is what makes compress/decompress round trips byte-exact.
 
@@ -132,6 +133,55 @@ def forward_stepped(weights: dict, last_token: int, state: State) -> torch.Tenso
     return forward_stepped_batched(weights, [int(last_token)], state).reshape(-1)
 
 
+_STEP_GRAPHS: dict = {}
+
+
+def forward_stepped_graphed(weights: dict, last_token: int, state: State) -> torch.Tensor:
+    """forward_stepped replayed from one captured HIP graph (the role of
+    cpp_path.py:369-410): embedding lookup, all layers and the head of one
+    token. The graph is captured on the first call for (weights, state) and
+    replayed after; capturing executes nothing, so every call advances the
+    state exactly once (the reference's per-layer capture advances it three
+    times on the first call, which its docstring records as broken). Same
+    bits as forward_stepped. Returns fp16 logits [V]."""
+    P: Prepared = weights["prepared"]
+    assert state.B == 1, "forward_stepped_graphed decodes one stream"
+    key = (id(weights), state.ptr)
+    hit = _STEP_GRAPHS.get(key)
+    if hit is None:
+        dev = P.device
+        ids = torch.zeros(1, dtype=torch.int32, device=dev)
+        x = torch.empty((16, P.C), dtype=torch.float16, device=dev)
+        xn = torch.empty((16, P.C), dtype=torch.float16, device=dev)
+        logits = torch.empty((1, P.V), dtype=torch.float16, device=dev)
+        ws, nbytes = workspace(weights, 16)
+        ws = ws.clone()        # private to the graph: the shared workspace may grow
+        torch.cuda.synchronize(dev)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            s = _lib.stream_ptr()
+            _lib.call("kr_embed", P.ptr, ids.data_ptr(), 1, x.data_ptr(), s)
+            _lib.call("kr_forward_layers", P.ptr, x.data_ptr(), 1, 1, state.ptr, ws.data_ptr(),
+                      nbytes, s)
+            _lib.call("kr_head_logits", P.ptr, x.data_ptr(), 1, xn.data_ptr(), logits.data_ptr(),
+                      P.V, s)
+        hit = (graph, ids, x, xn, logits, ws)
+        _STEP_GRAPHS[key] = hit
+    graph, ids, _, _, logits, _ = hit
+    tok = int(last_token)
+    if not 0 <= tok < P.V:
+        raise ValueError(f"token id out of range [0, {P.V})")
+    ids.fill_(tok)
+    graph.replay()
+    return logits.reshape(-1).clone()
+
+
+def clear_graph_cache():
+    """Drop the graphs forward_stepped_graphed captured (call when weights or
+    state buffers are freed)."""
+    _STEP_GRAPHS.clear()
+
+
 def softmax_cdfs_per_row(logits_TxV: torch.Tensor) -> torch.Tensor:
     """fp16 logits [T, V] -> int32 CDF [T, V+1] (softmax + cdf.py + scan, one kernel)."""
     from krunch_amd import krunch_ac_hip
@@ -146,20 +196,32 @@ def cpp_path_enabled() -> bool:
     return True
 
 
-def compute_decompress_batch(n_chunks: int = -1, default: int = 256) -> int:
-    """Streams decoded in lockstep. The fused decode step runs one 1024-thread
-    workgroup per stream, so 256 streams fill the 256 CUs of one MI355X once;
-    memory per stream is ~0.5 MB (state, logits, workspace), so HBM never
-    binds. Override with KRUNCH_DECOMPRESS_BATCH (cpp_path.py:531-580)."""
-    env = os.environ.get("KRUNCH_DECOMPRESS_BATCH")
-    upper = default
+# Streams per lockstep call, for compress and decompress alike (the role of
+# cpp_path.py:531-580, sized for MI355X by measurement rather than by CU
+# count). Decompress at the config-5 window on one MI355X: B = 128, 256, 384,
+# 512 give 1,074, 1,799, 1,857, 2,283 KB/s. 512 rows is the largest batch the
+# fused stepped kernels take (small-M GEMMs, fragment-packed operands), and
+# B x 1024-token windows stay under the forward's 2^31 / F row limit.
+DEFAULT_STREAM_BATCH = 512
+
+
+def env_batch(name: str, n_chunks: int, default: int) -> int:
+    B = default
+    env = os.environ.get(name)
     if env:
         try:
-            upper = max(1, int(env))
+            B = max(1, int(env))
         except ValueError:
             pass
-    return max(1, min(n_chunks, upper)) if n_chunks > 0 else upper
+    return max(1, min(n_chunks, B)) if n_chunks > 0 else B
 
 
-def pick_decompress_batch(default: int = 256) -> int:
+def compute_decompress_batch(n_chunks: int = -1, default: int = DEFAULT_STREAM_BATCH) -> int:
+    """Streams decoded in one lockstep call, clamped to n_chunks when given;
+    $KRUNCH_DECOMPRESS_BATCH overrides (cpp_path.py:531-580). Memory is never
+    the limit: ~0.5 MB per stream (state, logits, workspace) against 288 GB."""
+    return env_batch("KRUNCH_DECOMPRESS_BATCH", n_chunks, default)
+
+
+def pick_decompress_batch(default: int = DEFAULT_STREAM_BATCH) -> int:
     return compute_decompress_batch(n_chunks=-1, default=default)

@@ -13,6 +13,9 @@
 // Packed (T tokens per stream) and stepped (T = 1) calls run the same
 // kernels, so every row is computed by the same instruction sequence.
 #include <algorithm>
+#include <cstdlib>
+#include <cstring>
+#include <mutex>
 #include <vector>
 
 #include "kr_gemm.h"
@@ -739,6 +742,21 @@ bool use_fragments(const kr_layer_weights& L, long long M) {
     return M <= KR_GEMM_SMALL_M && L.Kf && L.Vf && L.Rf && L.Of && L.fKf && L.fVf && L.fRf;
 }
 
+// Phase marks for the layer profiler: event i is recorded on the stream
+// before phase i starts (i = 0..6) and event 7 after the last one. Phases:
+// ln1_mix, kvr_matmul, wkv, ow_matmul_residual, ln2_mix, ffn_rk_matmul,
+// ffn_v_matmul_residual. A fused launch that covers two phases leaves the
+// second one empty. ev == nullptr records nothing.
+struct Phases {
+    hipEvent_t* ev = nullptr;
+    hipStream_t s = nullptr;
+    int mark(int i) const {
+        if (!ev) return KR_OK;
+        KR_HIP(hipEventRecord(ev[i], s));
+        return KR_OK;
+    }
+};
+
 // w8a8 layer: the same op order with the seven products on
 // int8 MFMA. LN-mix writes its operands quantised per row; the WKV output and
 // the ReLU^2 output are quantised by a row kernel before their products.
@@ -770,7 +788,7 @@ inline void set_embed(LnMixArgs& a, const EmbedSrc* e, kr_half* x) {
 
 int layer_forward_q8(const kr_layer_weights& L, int C, int F, kr_half* x, int B, int T,
                      const kr_layer_state& st, const Work& w, hipStream_t s,
-                     const EmbedSrc* e) {
+                     const EmbedSrc* e, const Phases& ph) {
     const kr_layer_q8& Q = *L.q8;
     const int M = B * T, G = C / 256;
     const bool fr = M <= KR_GEMM_SMALL_M && Q.K.qf && Q.V.qf && Q.R.qf && Q.O.qf && Q.fK.qf &&
@@ -788,8 +806,10 @@ int layer_forward_q8(const kr_layer_weights& L, int C, int F, kr_half* x, int B,
     a.run = rows_per_run(T);
     a.frag = fr ? 1 : 0;
     set_embed(a, e, x);
+    KR_TRY(ph.mark(0));
     KR_TRY(launch_ln_mix<3>(G, a, s));
     set_embed(a, nullptr, x);
+    KR_TRY(ph.mark(1));
     {
         const kr_gemm_args jobs[3] = {gemm_q8(w.kx8, w.kxs, M, C, Q.K, C, w.k, fr),
                                       gemm_q8(w.vx8, w.vxs, M, C, Q.V, C, w.v, fr),
@@ -797,6 +817,7 @@ int layer_forward_q8(const kr_layer_weights& L, int C, int F, kr_half* x, int B,
         const int eps[3] = {KR_EP_F32, KR_EP_F32, KR_EP_SIGMOID};
         KR_TRY(kr_gemm_launch_multi(jobs, eps, 3, s));
     }
+    KR_TRY(ph.mark(2));
     {
         dim3 grid((C + 255) / 256, B);
         wkv_kernel<<<grid, 256, 0, s>>>(w.k, w.v, w.r, L.decay, L.first, st.aa, st.bb, st.pp,
@@ -804,7 +825,9 @@ int layer_forward_q8(const kr_layer_weights& L, int C, int F, kr_half* x, int B,
         KR_LAUNCHED();
     }
     KR_TRY(kr_impl_quantize_rows(w.ry, C, M, C, w.ry8, w.rys, fr ? 1 : 0, s));
+    KR_TRY(ph.mark(3));
     KR_TRY(kr_gemm_launch(gemm_q8(w.ry8, w.rys, M, C, Q.O, C, x, fr, x), KR_EP_RESID, s));
+    KR_TRY(ph.mark(4));
     a.ln_w = H(L.ln2_w);
     a.ln_b = H(L.ln2_b);
     a.tm[0] = H(L.ftm_k); a.tm[1] = H(L.ftm_r);
@@ -812,6 +835,7 @@ int layer_forward_q8(const kr_layer_weights& L, int C, int F, kr_half* x, int B,
     a.qs[0] = w.fkxs; a.qs[1] = w.frxs;
     a.state = Hm(st.ffn_xx);
     KR_TRY(launch_ln_mix<2>(G, a, s));
+    KR_TRY(ph.mark(5));
     {
         const kr_gemm_args jobs[2] = {gemm_q8(w.frx8, w.frxs, M, C, Q.fR, C, w.rf, fr),
                                       gemm_q8(w.fkx8, w.fkxs, M, C, Q.fK, F, w.kf, fr)};
@@ -819,8 +843,9 @@ int layer_forward_q8(const kr_layer_weights& L, int C, int F, kr_half* x, int B,
         KR_TRY(kr_gemm_launch_multi(jobs, eps, 2, s));
     }
     KR_TRY(kr_impl_quantize_rows(w.kf, F, M, F, w.kf8, w.kfs, fr ? 1 : 0, s));
+    KR_TRY(ph.mark(6));
     KR_TRY(kr_gemm_launch(gemm_q8(w.kf8, w.kfs, M, F, Q.fV, C, x, fr, x, w.rf), KR_EP_GATED, s));
-    return KR_OK;
+    return ph.mark(7);
 }
 
 // Stepped (T = 1) fp16 layer with fragment-packed weights: LN1-mix, the
@@ -843,7 +868,7 @@ constexpr int kStageBlocks = 512;   // staging workgroups per LN-mix launch (64 
 
 int layer_step_fused(const kr_layer_weights& L, int C, int F, kr_half* x, int B,
                      const kr_layer_state& st, const Work& w, hipStream_t s,
-                     const EmbedSrc* e) {
+                     const EmbedSrc* e, const Phases& ph) {
     const int M = B, G = C / 256;
     // Weights the next products read, staged into their XCDs' L2 by the
     // LN-mix launches (which wait on memory latency, not bandwidth): LN1 stages
@@ -877,8 +902,10 @@ int layer_step_fused(const kr_layer_weights& L, int C, int F, kr_half* x, int B,
     a.frag = 1;
     set_embed(a, e, x);
     a.pf = pf_att;
+    KR_TRY(ph.mark(0));
     KR_TRY(launch_ln_mix<3>(G, a, s));
     set_embed(a, nullptr, x);
+    KR_TRY(ph.mark(1));
     KvrWkvArgs kw{};
     kw.A[0] = w.kx; kw.A[1] = w.vx; kw.A[2] = w.rx;
     kw.Wf[0] = H(L.Kf); kw.Wf[1] = H(L.Vf); kw.Wf[2] = H(L.Rf);
@@ -890,7 +917,10 @@ int layer_step_fused(const kr_layer_weights& L, int C, int F, kr_half* x, int B,
     kw.ry = w.ry;
     kw.M = M;
     KR_TRY(launch_kvr_wkv(G, kw, s));
+    KR_TRY(ph.mark(2));
+    KR_TRY(ph.mark(3));      // WKV ran inside the K/V/R launch
     KR_TRY(kr_gemm_launch(gemm_args(w.ry, M, C, L.Ot, C, x, x, nullptr, L.Of, true), KR_EP_RESID, s));
+    KR_TRY(ph.mark(4));
     a.ln_w = H(L.ln2_w);
     a.ln_b = H(L.ln2_b);
     a.tm[0] = H(L.ftm_k); a.tm[1] = H(L.ftm_r);
@@ -898,6 +928,7 @@ int layer_step_fused(const kr_layer_weights& L, int C, int F, kr_half* x, int B,
     a.state = Hm(st.ffn_xx);
     a.pf = pf_ffn;
     KR_TRY(launch_ln_mix<2>(G, a, s));
+    KR_TRY(ph.mark(5));
     {
         const kr_gemm_args jobs[2] = {
             gemm_args(w.frx, M, C, L.fRt, C, w.rf, nullptr, nullptr, L.fRf, true),
@@ -905,17 +936,18 @@ int layer_step_fused(const kr_layer_weights& L, int C, int F, kr_half* x, int B,
         const int eps[2] = {KR_EP_SIGMOID, KR_EP_RELUSQ};
         KR_TRY(kr_gemm_launch_multi(jobs, eps, 2, s));
     }
+    KR_TRY(ph.mark(6));
     KR_TRY(kr_gemm_launch(gemm_args(w.kf, M, F, L.fVt, C, x, x, w.rf, L.fVf, true), KR_EP_GATED, s));
-    return KR_OK;
+    return ph.mark(7);
 }
 
 int layer_forward(const kr_layer_weights& L, int C, int F, kr_half* x, int B, int T,
                   const kr_layer_state& st, const Work& w, hipStream_t s,
-                  const EmbedSrc* e = nullptr) {
-    if (L.q8) return layer_forward_q8(L, C, F, x, B, T, st, w, s, e);
+                  const EmbedSrc* e = nullptr, const Phases& ph = Phases{}) {
+    if (L.q8) return layer_forward_q8(L, C, F, x, B, T, st, w, s, e, ph);
     const int M = B * T, G = C / 256;
     const bool fr = use_fragments(L, M);
-    if (fr && T == 1) return layer_step_fused(L, C, F, x, B, st, w, s, e);
+    if (fr && T == 1) return layer_step_fused(L, C, F, x, B, st, w, s, e, ph);
     LnMixArgs a{};
     a.x = x;
     a.ln_w = H(L.ln1_w);
@@ -928,8 +960,10 @@ int layer_forward(const kr_layer_weights& L, int C, int F, kr_half* x, int B, in
     a.run = rows_per_run(T);
     a.frag = fr ? 1 : 0;
     set_embed(a, e, x);
+    KR_TRY(ph.mark(0));
     KR_TRY(launch_ln_mix<3>(G, a, s));
     set_embed(a, nullptr, x);
+    KR_TRY(ph.mark(1));
     {
         const kr_gemm_args jobs[3] = {
             gemm_args(w.kx, M, C, L.Kt, C, w.k, nullptr, nullptr, L.Kf, fr),
@@ -938,19 +972,23 @@ int layer_forward(const kr_layer_weights& L, int C, int F, kr_half* x, int B, in
         const int eps[3] = {KR_EP_F32, KR_EP_F32, KR_EP_SIGMOID};
         KR_TRY(kr_gemm_launch_multi(jobs, eps, 3, s));
     }
+    KR_TRY(ph.mark(2));
     {
         dim3 grid((C + 255) / 256, B);
         wkv_kernel<<<grid, 256, 0, s>>>(w.k, w.v, w.r, L.decay, L.first, st.aa, st.bb, st.pp,
                                         w.ry, B, T, C, fr ? 1 : 0);
         KR_LAUNCHED();
     }
+    KR_TRY(ph.mark(3));
     KR_TRY(kr_gemm_launch(gemm_args(w.ry, M, C, L.Ot, C, x, x, nullptr, L.Of, fr), KR_EP_RESID, s));
+    KR_TRY(ph.mark(4));
     a.ln_w = H(L.ln2_w);
     a.ln_b = H(L.ln2_b);
     a.tm[0] = H(L.ftm_k); a.tm[1] = H(L.ftm_r);
     a.out[0] = w.fkx; a.out[1] = w.frx;
     a.state = Hm(st.ffn_xx);
     KR_TRY(launch_ln_mix<2>(G, a, s));
+    KR_TRY(ph.mark(5));
     {
         const kr_gemm_args jobs[2] = {
             gemm_args(w.frx, M, C, L.fRt, C, w.rf, nullptr, nullptr, L.fRf, fr),
@@ -958,8 +996,9 @@ int layer_forward(const kr_layer_weights& L, int C, int F, kr_half* x, int B, in
         const int eps[2] = {KR_EP_SIGMOID, KR_EP_RELUSQ};
         KR_TRY(kr_gemm_launch_multi(jobs, eps, 2, s));
     }
+    KR_TRY(ph.mark(6));
     KR_TRY(kr_gemm_launch(gemm_args(w.kf, M, F, L.fVt, C, x, x, w.rf, L.fVf, fr), KR_EP_GATED, s));
-    return KR_OK;
+    return ph.mark(7);
 }
 
 int check_model(const kr_model_weights* m) {
@@ -983,6 +1022,54 @@ kr_layer_state state_of(void* state, int layer, int B, int C) {
     st.bb = reinterpret_cast<float*>(p + (size_t)B * C * 8);
     st.pp = reinterpret_cast<float*>(p + (size_t)B * C * 12);
     return st;
+}
+
+// ---------------------------------------------------------------------------
+// Layer phase profiler (the role of layer_cpp.cpp:111-157): when on, each
+// kr_layer_step call records HIP events between its phases on its stream,
+// waits for the last one and adds the elapsed times to running sums. Off by
+// default; KRUNCH_PHASE_PROFILE=1 turns it on at first use, kr_phase_profile
+// at any time. Calls made during stream capture are never profiled.
+// ---------------------------------------------------------------------------
+constexpr int kPhases = 7;
+const char* const kPhaseNames[kPhases] = {"ln1_mix", "kvr_matmul", "wkv", "ow_matmul_residual",
+                                          "ln2_mix", "ffn_rk_matmul", "ffn_v_matmul_residual"};
+
+struct PhaseProfiler {
+    std::mutex mu;
+    int enabled = -1;               // -1: not decided yet (read the environment)
+    int dev = -1;                   // device the events belong to
+    hipEvent_t ev[kPhases + 1] = {};
+    double sum_ms[kPhases] = {};
+    long long calls = 0;
+};
+PhaseProfiler g_prof;
+
+// with g_prof.mu held
+int profile_state() {
+    if (g_prof.enabled < 0) {
+        const char* e = std::getenv("KRUNCH_PHASE_PROFILE");
+        g_prof.enabled = (e && std::strcmp(e, "1") == 0) ? 1 : 0;
+    }
+    return g_prof.enabled;
+}
+
+bool profile_on() {
+    std::lock_guard<std::mutex> lock(g_prof.mu);
+    return profile_state() == 1;
+}
+
+// with g_prof.mu held: events on the current device
+int profile_events() {
+    int dev = 0;
+    KR_HIP(hipGetDevice(&dev));
+    if (g_prof.dev == dev && g_prof.ev[0]) return KR_OK;
+    for (auto& e : g_prof.ev)
+        if (e) { (void)hipEventDestroy(e); e = nullptr; }
+    g_prof.dev = -1;
+    for (auto& e : g_prof.ev) KR_HIP(hipEventCreate(&e));
+    g_prof.dev = dev;
+    return KR_OK;
 }
 
 }  // namespace
@@ -1128,7 +1215,53 @@ int kr_layer_step(const kr_layer_weights* L, int C, int F, void* x, int B, int T
     const long long M = (long long)B * T;
     KR_REQUIRE(ws_bytes >= work_bytes(M, C, F), "kr_layer_step: workspace too small");
     kr_layer_state st{att_xx, aa, bb, pp, ffn_xx};
-    return layer_forward(*L, C, F, Hm(x), B, T, st, carve(ws, M, C, F), kr_stream(stream));
+    const hipStream_t s = kr_stream(stream);
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    KR_HIP(hipStreamIsCapturing(s, &cap));
+    if (!profile_on() || cap != hipStreamCaptureStatusNone)
+        return layer_forward(*L, C, F, Hm(x), B, T, st, carve(ws, M, C, F), s);
+    // Profiled call: events between the phases, then a wait for the last one
+    // (one synchronisation per call, as the reference's profiler does).
+    std::lock_guard<std::mutex> lock(g_prof.mu);
+    KR_TRY(profile_events());
+    Phases ph;
+    ph.ev = g_prof.ev;
+    ph.s = s;
+    KR_TRY(layer_forward(*L, C, F, Hm(x), B, T, st, carve(ws, M, C, F), s, nullptr, ph));
+    KR_HIP(hipEventSynchronize(g_prof.ev[kPhases]));
+    for (int i = 0; i < kPhases; i++) {
+        float ms = 0.f;
+        KR_HIP(hipEventElapsedTime(&ms, g_prof.ev[i], g_prof.ev[i + 1]));
+        g_prof.sum_ms[i] += ms;
+    }
+    g_prof.calls++;
+    return KR_OK;
+}
+
+int kr_phase_profile(int enable) {
+    std::lock_guard<std::mutex> lock(g_prof.mu);
+    const int before = profile_state();
+    if (enable == 0 || enable == 1) g_prof.enabled = enable;
+    return before;
+}
+
+int kr_phase_count(void) { return kPhases; }
+
+const char* kr_phase_name(int i) { return (i >= 0 && i < kPhases) ? kPhaseNames[i] : nullptr; }
+
+int kr_read_phase_times(double* ms, int n, long long* call_count) {
+    KR_REQUIRE(ms || n == 0, "kr_read_phase_times: null pointer");
+    std::lock_guard<std::mutex> lock(g_prof.mu);
+    for (int i = 0; i < n && i < kPhases; i++) ms[i] = g_prof.sum_ms[i];
+    if (call_count) *call_count = g_prof.calls;
+    return KR_OK;
+}
+
+int kr_reset_phase_times(void) {
+    std::lock_guard<std::mutex> lock(g_prof.mu);
+    for (double& v : g_prof.sum_ms) v = 0.0;
+    g_prof.calls = 0;
+    return KR_OK;
 }
 
 int kr_wkv(int B, int T, int C, const float* decay, const float* first, const float* k,

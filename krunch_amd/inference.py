@@ -41,34 +41,49 @@ BOS_TOKEN = 0
 CDF_PRECISION = 24
 
 
-# Streams per lockstep call (the role of cpp_path.py:531-580
-# compute_decompress_batch, sized for MI355X by measurement rather than by
-# SM count). Decompress at the config-5 window on one MI355X: B = 128, 256,
-# 384, 512 give 1,074, 1,799, 1,857, 2,283 KB/s. 512 rows is the largest batch
-# the fused stepped kernels take (small-M GEMMs, fragment-packed operands),
-# and B x 1024-token windows stay under the forward's 2^31 / F row limit.
-DEFAULT_STREAM_BATCH = 512
+DEFAULT_STREAM_BATCH = cpp_path.DEFAULT_STREAM_BATCH
+
+# Rows per head GEMM + CDF block of a compress window: the logits buffer
+# holds this many rows (4096 x 50280 fp16 = 412 MB); 4096-row blocks keep the
+# head on the persistent 256x128 GEMM kernel.
+HEAD_ROWS = 4096
+
+# Largest coder buffer of one lockstep call, in bytes. Stream offsets into it
+# are int32 and its length is a uint32 in the C ABI (the reference's
+# base_byte_offsets are int32 too, encode_kernel.cu:148-197), so a call whose
+# concatenated bitstreams would exceed 2^31 - 1 bytes is split into several.
+MAX_CALL_BYTES = (1 << 31) - 1
 
 
-def _env_batch(name: str, n_chunks: int, default: int) -> int:
-    B = default
-    env = os.environ.get(name)
-    if env:
-        try:
-            B = max(1, int(env))
-        except ValueError:
-            pass
-    return max(1, min(n_chunks, B)) if n_chunks > 0 else B
+def coder_stream_cap(n_tokens: int) -> int:
+    """Output bytes reserved per stream for n_tokens symbols. A symbol costs at
+    most CDF_PRECISION + 2 bits plus pending bits that the same budget covers;
+    4 bytes per token + 64 bounds every stream (an overflow raises)."""
+    return int(4 * n_tokens + 64)
 
 
-def compute_decompress_batch(n_chunks: int = -1, default: int = DEFAULT_STREAM_BATCH) -> int:
-    """Streams decoded in one lockstep call; $KRUNCH_DECOMPRESS_BATCH overrides."""
-    return _env_batch("KRUNCH_DECOMPRESS_BATCH", n_chunks, default)
+def split_by_bytes(sizes: Sequence[int], limit: int) -> List[range]:
+    """Consecutive index ranges whose byte sizes sum to <= limit each (one
+    item per range at least; an item larger than limit is an error)."""
+    out, start, acc = [], 0, 0
+    for i, n in enumerate(sizes):
+        if n > limit:
+            raise ValueError(f"one stream needs {n} coder bytes > the per-call limit {limit}")
+        if acc + n > limit and i > start:
+            out.append(range(start, i))
+            start, acc = i, 0
+        acc += n
+    if len(sizes) > start:
+        out.append(range(start, len(sizes)))
+    return out
+
+
+compute_decompress_batch = cpp_path.compute_decompress_batch
 
 
 def compute_compress_batch(n_chunks: int = -1, default: int = DEFAULT_STREAM_BATCH) -> int:
     """Streams compressed in one packed call; $KRUNCH_COMPRESS_BATCH overrides."""
-    return _env_batch("KRUNCH_COMPRESS_BATCH", n_chunks, default)
+    return cpp_path.env_batch("KRUNCH_COMPRESS_BATCH", n_chunks, default)
 
 
 def encode_header(original_len: int, n_chunks: int, crc32: int, adapter_id: int = 0,
@@ -101,6 +116,7 @@ class InferenceEngine:
         # group measured fastest on MI355X (branches of one graph do not overlap)
         self.decode_groups = int(os.environ.get("KRUNCH_DECODE_GROUPS", "1"))
         self.model_id = MODEL_ID
+        self.max_call_bytes = MAX_CALL_BYTES
 
     # ------------------------------------------------------------------ setup
     def load(self, weights: Optional[dict] = None, tokenizer_path: Optional[str] = None,
@@ -146,7 +162,16 @@ class InferenceEngine:
         B = len(token_streams)
         if B == 0:
             return []
-        cap = compute_compress_batch(B)
+        lens = np.array([len(t) for t in token_streams], dtype=np.int64)
+        if (lens < 1).any():
+            raise ValueError("chunk has no tokens")
+        Tmax = int(lens.max())
+        per_cap = coder_stream_cap(Tmax)
+        # streams per call: the batch size, and a coder buffer of <= max_call_bytes
+        cap = min(compute_compress_batch(B), max(1, self.max_call_bytes // per_cap))
+        if per_cap > self.max_call_bytes:
+            raise ValueError(f"a {Tmax}-token stream needs {per_cap} coder bytes > the "
+                             f"per-call limit {self.max_call_bytes}")
         if B > cap:
             res: List[bytes] = []
             for i in range(0, B, cap):
@@ -156,10 +181,6 @@ class InferenceEngine:
         W = self._weights
         P = W["prepared"]
         dev = P.device
-        lens = np.array([len(t) for t in token_streams], dtype=np.int64)
-        if (lens < 1).any():
-            raise ValueError("chunk has no tokens")
-        Tmax = int(lens.max())
         tok = np.zeros((B, Tmax), dtype=np.int32)
         for b, t in enumerate(token_streams):
             tok[b, :len(t)] = np.asarray(t, dtype=np.int32)
@@ -171,8 +192,8 @@ class InferenceEngine:
         tok_d = torch.from_numpy(tok).to(dev)
         inp_d = torch.from_numpy(inp).to(dev)
 
-        per_cap = int(4 * Tmax + 64)
         out = torch.zeros(B * per_cap, dtype=torch.uint8, device=dev)
+        out_cap = _lib.u32(out.numel(), "coder buffer bytes")
         base = torch.arange(B, dtype=torch.int32, device=dev) * per_cap
         ac = torch.zeros((B, 4), dtype=torch.int64)
         ac[:, 1] = 0xFFFFFFFF
@@ -183,7 +204,7 @@ class InferenceEngine:
         M = B * Tw
         ws, nbytes = cpp_path.workspace(W, M)
         x = torch.empty((M, P.C), dtype=torch.float16, device=dev)
-        head_rows = min(M, 2048)
+        head_rows = min(M, HEAD_ROWS)
         ld = cpp_path.logits_ld(P.V)
         logits = torch.empty((head_rows, ld), dtype=torch.float16, device=dev)
         lens_d = torch.from_numpy(lens.astype(np.int32)).to(dev)
@@ -213,11 +234,11 @@ class InferenceEngine:
             fwd_done[i % 2].record(main)
             enc.wait_event(fwd_done[i % 2])
             _lib.call("kr_encode_pairs_batched", buf.data_ptr(), T, T, n_valid[i].data_ptr(),
-                      out.data_ptr(), out.numel(), base.data_ptr(), ac.data_ptr(), B,
+                      out.data_ptr(), out_cap, base.data_ptr(), ac.data_ptr(), B,
                       CDF_PRECISION, err.data_ptr(), enc.cuda_stream)
             enc_done[i % 2].record(enc)
         main.wait_stream(enc)
-        _lib.call("kr_encode_finalize_batched", out.data_ptr(), out.numel(), base.data_ptr(),
+        _lib.call("kr_encode_finalize_batched", out.data_ptr(), out_cap, base.data_ptr(),
                   ac.data_ptr(), B, err.data_ptr(), s)
         if int(err.item()):
             raise RuntimeError("range coder output buffer overflow")
@@ -240,10 +261,15 @@ class InferenceEngine:
         if B == 0:
             return []
         cap = compute_decompress_batch(B)
-        if B > cap:
+        # calls of <= cap streams whose concatenated bitstreams (+1 pad byte)
+        # fit the int32 offsets / uint32 length of the decoder interface
+        parts = [r for g in split_by_bytes([len(e) - 8 + 1 for e in encoded_chunks],
+                                           self.max_call_bytes)
+                 for r in (range(i, min(i + cap, g.stop)) for i in range(g.start, g.stop, cap))]
+        if len(parts) > 1:
             res: List[np.ndarray] = []
-            for i in range(0, B, cap):
-                res += self.decompress_tokens_batched(encoded_chunks[i:i + cap])
+            for r in parts:
+                res += self.decompress_tokens_batched(encoded_chunks[r.start:r.stop])
             return res
         W = self._weights
         P = W["prepared"]
@@ -256,11 +282,12 @@ class InferenceEngine:
         offs = np.cumsum([0] + [len(s) for s in streams])
         cat = np.frombuffer(b"".join(streams) + b"\0", dtype=np.uint8)
         inbuf = torch.from_numpy(cat.copy()).to(dev)
+        in_len = _lib.u32(inbuf.numel(), "decoder input bytes")
         base = torch.from_numpy(offs[:-1].astype(np.int32)).to(dev)
         limits = torch.from_numpy(np.array([len(s) for s in streams], dtype=np.int32)).to(dev)
         ac = torch.empty((B, 4), dtype=torch.uint32, device=dev)
         s = _lib.stream_ptr()
-        _lib.call("kr_decode_init_batched", inbuf.data_ptr(), inbuf.numel(), base.data_ptr(),
+        _lib.call("kr_decode_init_batched", inbuf.data_ptr(), in_len, base.data_ptr(),
                   limits.data_ptr(), ac.data_ptr(), B, s)
         Tmax = max(n_tok)
         state = State(P.n_layer, B, P.C, dev)
@@ -275,7 +302,7 @@ class InferenceEngine:
         ld = cpp_path.logits_ld(P.V)
         logits = torch.empty((B, ld), dtype=torch.float16, device=dev)
         _lib.call("kr_decode_run", P.ptr, B, state.ptr, syms.data_ptr(), x.data_ptr(),
-                  ws.data_ptr(), nbytes, logits.data_ptr(), ld, inbuf.data_ptr(), inbuf.numel(),
+                  ws.data_ptr(), nbytes, logits.data_ptr(), ld, inbuf.data_ptr(), in_len,
                   base.data_ptr(), limits.data_ptr(), ac.data_ptr(), tokens.data_ptr(), Tmax,
                   count.data_ptr(), ntd.data_ptr(), CDF_PRECISION, Tmax, G,
                   1 if self.use_graph else 0, s)

@@ -72,3 +72,27 @@ def test_stream_batch_sizing(monkeypatch):
     assert inf.compute_decompress_batch(1000) == 512
     monkeypatch.setenv("KRUNCH_COMPRESS_BATCH", "0")
     assert inf.compute_compress_batch(9) == 1
+
+
+def test_coder_call_split_sizing():
+    """Calls are split so the concatenated bitstreams of one call fit the
+    int32 stream offsets / uint32 length of the C ABI."""
+    from krunch_amd import _lib
+    from krunch_amd import inference as inf
+    assert inf.MAX_CALL_BYTES == 2 ** 31 - 1
+    assert inf.coder_stream_cap(1024) == 4 * 1024 + 64
+    parts = inf.split_by_bytes([5, 5, 5, 5, 5], 10)
+    assert [list(r) for r in parts] == [[0, 1], [2, 3], [4]]
+    assert [list(r) for r in inf.split_by_bytes([3, 9, 1, 1], 10)] == [[0], [1, 2], [3]]
+    assert inf.split_by_bytes([], 10) == []
+    with pytest.raises(ValueError):
+        inf.split_by_bytes([11], 10)
+    # 512 streams of 262,144 tokens: 537 MB per call, far under the limit; a
+    # 1 GB-per-stream call is split
+    per = inf.coder_stream_cap(262144)
+    assert 512 * per < inf.MAX_CALL_BYTES
+    assert inf.MAX_CALL_BYTES // inf.coder_stream_cap(2 ** 28) == 1
+    assert _lib.u32(2 ** 32 - 1) == 2 ** 32 - 1
+    for bad in (2 ** 32, 2 ** 32 + 5, -1):
+        with pytest.raises(ValueError):
+            _lib.u32(bad)

@@ -1,0 +1,153 @@
+"""Every BASELINE.json configuration at its real shape, against the oracle.
+
+The compress window of a real config runs kernels no toy-shape test reaches:
+the persistent 256x128 GEMM with its vectorised epilogues (M = B*T >= 4096),
+the packed WKV over T = 1024, the head and CDF in 4096-row blocks. These tests
+check them where exactness is defined:
+  * logits of sampled streams within 1e-2 max-abs of the fp32 oracle
+    (rows are batch-invariant, so the oracle runs on those streams alone);
+  * payloads == the oracle range coder fed the oracle CDF of the GPU logits;
+  * stepped logits == packed logits bit for bit at every decode step;
+  * byte-exact round trips at the config's B and length.
+Streams are synthetic Zipf(1.1) token ids on the 169M-shaped random-init
+model."""
+import numpy as np
+import pytest
+import torch
+
+from krunch_amd import cpp_path, synthetic
+from krunch_amd import krunch_ac_hip as ops
+from krunch_amd.inference import InferenceEngine
+from oracle import range_coder as orc
+from oracle import rwkv4
+from oracle import softmax as osm
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+@pytest.fixture(scope="module")
+def w16():
+    return synthetic.make_weights()
+
+
+@pytest.fixture(scope="module")
+def eng(w16):
+    return InferenceEngine().load(w16)
+
+
+def _oracle_logits(w16, toks):
+    st = rwkv4.new_state(12, toks.shape[0], 768)
+    return rwkv4.forward(w16, torch.as_tensor(synthetic.model_inputs(toks)), st).numpy()
+
+
+def _check_payload(payload, logits16, toks):
+    """payload == oracle coder on the oracle CDF of these fp16 logits."""
+    assert payload[8:] == orc.encode(osm.logits_to_cdf(logits16), toks)
+
+
+def test_config2_packed_B64_T1024_vs_oracle(eng, w16):
+    """Config 2: one packed window of 64 chunks x 1024 tokens (M = 65,536)."""
+    B, T = 64, 1024
+    toks = synthetic.zipf_tokens(B, T, seed_base=2000)
+    enc = eng.compress_tokens_batched(list(toks))
+    W = eng.weights
+    st = cpp_path.fresh_state_batched(W, B)
+    logits = cpp_path.forward_packed_batched(W, synthetic.model_inputs(toks), st).view(B, T, -1)
+    sel = [0, B - 1]
+    got = logits[sel].cpu().numpy()
+    del logits
+    ref = _oracle_logits(w16, toks[sel])
+    err = np.abs(got.astype(np.float32) - ref).max()
+    assert err < 1e-2, f"config 2 logits vs fp32 oracle: max abs {err}"
+    for i, b in enumerate(sel):
+        _check_payload(enc[b], got[i], toks[b])
+
+
+def test_config3_stepped_B128_1024_steps(eng):
+    """Config 3: 128 streams decoded in lockstep for 1024 steps, byte-exact;
+    the stepped logits equal the packed logits bit for bit at every step, and
+    at sampled steps the decoded symbol's CDF interval from the full CDF of
+    the stepped row equals the interval the compress side encoded."""
+    B, T = 128, 1024
+    toks = synthetic.zipf_tokens(B, T, seed_base=3000)
+    enc = eng.compress_tokens_batched(list(toks))
+    dec = eng.decompress_tokens_batched(enc)
+    for t, d in zip(toks, dec):
+        np.testing.assert_array_equal(d, t)
+    W = eng.weights
+    inp = torch.as_tensor(synthetic.model_inputs(toks), device=DEV)
+    tok_d = torch.as_tensor(toks, device=DEV)
+    st = cpp_path.fresh_state_batched(W, B)
+    packed = cpp_path.forward_packed_batched(W, inp, st).view(B, T, -1)
+    st2 = cpp_path.fresh_state_batched(W, B)
+    sampled = {0, 1, 511, 1023}
+    for t in range(T):
+        stepped = cpp_path.forward_stepped_batched(W, inp[:, t], st2)
+        assert torch.equal(stepped, packed[:, t]), f"step {t}"
+        if t in sampled:
+            cdf = ops.softmax_cdf(stepped)                      # decode side, full rows
+            sym = tok_d[:, t].to(torch.int32).contiguous()
+            pairs = torch.empty((B, 2), dtype=torch.int32, device=DEV)
+            rows = packed[:, t].contiguous()                    # compress side
+            from krunch_amd import _lib
+            _lib.call("kr_softmax_cdf_pairs", rows.data_ptr(), B, rows.shape[1], rows.shape[1],
+                      sym.data_ptr(), pairs.data_ptr(), 24, _lib.stream_ptr())
+            lo = cdf.gather(1, sym.long().unsqueeze(1)).squeeze(1)
+            hi = cdf.gather(1, sym.long().unsqueeze(1) + 1).squeeze(1)
+            assert torch.equal(pairs[:, 0], lo) and torch.equal(pairs[:, 1], hi), f"step {t}"
+    assert torch.equal(st.buf, st2.buf)
+
+
+def test_config4_w8a8_B256_T1024(eng, w16):
+    """Config 4: the w8a8 codec on 256 chunks x 1024 tokens (M = 262,144):
+    byte-exact round trip; bits/token within 0.5% of the fp16 codec's."""
+    B, T = 256, 1024
+    toks = synthetic.zipf_tokens(B, T, seed_base=4000)
+    e8 = InferenceEngine().load(w16, w8a8=True)
+    enc8 = e8.compress_tokens_batched(list(toks))
+    dec8 = e8.decompress_tokens_batched(enc8)
+    for t, d in zip(toks, dec8):
+        np.testing.assert_array_equal(d, t)
+    enc16 = eng.compress_tokens_batched(list(toks))
+    b8 = sum(len(e) - 8 for e in enc8)
+    b16 = sum(len(e) - 8 for e in enc16)
+    assert abs(b8 - b16) / b16 < 0.005, (8 * b8 / (B * T), 8 * b16 / (B * T))
+
+
+def test_config5_three_windows_with_repeats(eng, w16):
+    """Config 5 over three 1024-token windows (state carried across windows
+    on both sides) of 256 chunks with 5% repeated 64-token spans: byte-exact;
+    one stream's payload equals the oracle chain on the logits of a single
+    packed call over all 3072 tokens, and those logits are within 1e-2 of the
+    fp32 oracle (the carried state stays on track over three windows)."""
+    B, T = 256, 3072
+    toks = synthetic.zipf_tokens(B, T, repeat_rate=0.05, seed_base=5000)
+    enc = eng.compress_tokens_batched(list(toks))
+    dec = eng.decompress_tokens_batched(enc)
+    for t, d in zip(toks, dec):
+        np.testing.assert_array_equal(d, t)
+    W = eng.weights
+    b = B - 1
+    st = cpp_path.fresh_state_batched(W, 1)
+    got = cpp_path.forward_packed_batched(W, synthetic.model_inputs(toks[b:b + 1]), st)
+    got = got.cpu().numpy()
+    _check_payload(enc[b], got, toks[b])
+    ref = _oracle_logits(w16, toks[b:b + 1])[0]
+    err = np.abs(got.astype(np.float32) - ref).max()
+    assert err < 1e-2, f"config 5 logits vs fp32 oracle after 3 windows: max abs {err}"
+
+
+def test_config5_full_length_chunks(eng):
+    """Config 5's chunk length: 8 chunks of 262,144 tokens each (256 windows,
+    5% repeats), compressed with state carried across every window and
+    decoded in 262,144 lockstep steps: byte-exact. (The decode step is
+    latency-bound, so 8 streams take about as long as 256 would per step.)"""
+    B, T = 8, 262144
+    toks = synthetic.zipf_tokens(B, T, repeat_rate=0.05, seed_base=5500)
+    enc = eng.compress_tokens_batched(list(toks))
+    dec = eng.decompress_tokens_batched(enc)
+    for t, d in zip(toks, dec):
+        np.testing.assert_array_equal(d, t)
+    bpt = 8 * sum(len(e) - 8 for e in enc) / (B * T)
+    assert 8.0 < bpt < 17.0, bpt

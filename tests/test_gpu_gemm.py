@@ -52,11 +52,17 @@ def _run(ep, x, Wt, N, res=None, gate=None):
     return out
 
 
-def test_epilogues():
-    M, K, N = 333, 768, 768
-    x, W = _mk(M, K, N, 5)
+@pytest.mark.parametrize("M,K,N", [(333, 768, 768), (4096, 768, 768), (5000, 768, 3072),
+                                   (4096, 3072, 768), (8192 + 77, 768, 768)])
+def test_epilogues(M, K, N):
+    """Epilogues 2-5 (sigmoid, relu^2, residual, gated residual) on the tile
+    kernel (M = 333) and on the persistent 256x128 kernel every compress
+    window runs (M >= 4096, ragged last row tile at 8269), against torch
+    fp32 on the same accumulator."""
+    x, W = _mk(M, K, N, 5 + M)
     Wt = W.t().contiguous()
     acc = ops.det_matmul(x, W, torch.float32)
+    torch.testing.assert_close(acc, x.float() @ W.float(), rtol=1e-3, atol=1e-3)
     h = acc.half().float()
     res = torch.randn(M, N, device=DEV).half()
     gate = torch.rand(M, N, device=DEV).half()

@@ -154,3 +154,68 @@ def test_output_overflow_is_reported_not_written_past():
               st.data_ptr(), 24, err.data_ptr(), _lib.stream_ptr())
     assert int(err.item()) == 1
     assert int(guard.sum().item()) == 0
+
+
+def _ref_probs(N, V, seed):
+    """The reference coder tests' distribution recipe
+    (tests/test_ac_reference.py:14-18): uniform randoms, row-normalised."""
+    rng = np.random.default_rng(seed)
+    p = rng.random((N, V)).astype(np.float32)
+    return p / p.sum(axis=1, keepdims=True)
+
+
+@pytest.mark.parametrize("N,V,seed", [(1, 4, 10), (16, 64, 11), (256, 256, 12),
+                                      (1024, 1024, 13), (4096, 50277, 14)])
+def test_reference_shapes_roundtrip(N, V, seed):
+    """tests/test_ac_reference.py:63-75 on the GPU coder: symbols sampled
+    from the rows; CDF, bitstream and decode equal to the oracle's."""
+    from krunch_amd import krunch_ac
+    p = _ref_probs(N, V, seed)
+    rng = np.random.default_rng(seed + 100)
+    u = rng.random((N, 1)).astype(np.float32)
+    sym = (u < np.cumsum(p, axis=1)).argmax(axis=1).astype(np.int32)
+    cdf = krunch_ac.probs_to_cdf(p)
+    np.testing.assert_array_equal(cdf, ocdf.probs_to_cdf(p))
+    bits = krunch_ac.encode(cdf, sym)
+    assert bits == orc.encode(cdf, sym)
+    np.testing.assert_array_equal(krunch_ac.decode(bits, cdf), sym)
+
+
+def test_all_same_symbol_and_rare_symbol():
+    """tests/test_ac_reference.py:78-98: a stream of one symbol, and a
+    near-minimal-probability symbol (p = 1e-6) at every step."""
+    from krunch_amd import krunch_ac
+    p = _ref_probs(100, 50, 20)
+    sym = np.zeros(100, dtype=np.int32)
+    cdf = krunch_ac.probs_to_cdf(p)
+    bits = krunch_ac.encode(cdf, sym)
+    assert bits == orc.encode(cdf, sym)
+    np.testing.assert_array_equal(krunch_ac.decode(bits, cdf), sym)
+    V, N = 200, 50
+    p = np.full((N, V), 1e-6, dtype=np.float32)
+    p[:, 0] = 1.0 - 1e-6 * (V - 1)
+    p /= p.sum(axis=1, keepdims=True)
+    sym = np.full(N, 199, dtype=np.int32)
+    cdf = krunch_ac.probs_to_cdf(p)
+    np.testing.assert_array_equal(cdf, ocdf.probs_to_cdf(p))
+    # width floor(1e-6 * (2^24 - 200)) + 1 = 17 of 2^24
+    assert (np.diff(cdf[:, 199:201].astype(np.int64), axis=1) == 17).all()
+    bits = krunch_ac.encode(cdf, sym)
+    assert bits == orc.encode(cdf, sym)
+    np.testing.assert_array_equal(krunch_ac.decode(bits, cdf), sym)
+
+
+def test_compression_makes_progress():
+    """tests/test_ac_reference.py:111-121: a peaky distribution always
+    hitting its likely symbol codes far below the uniform 10 bits/symbol."""
+    from krunch_amd import krunch_ac
+    N, V = 2048, 1024
+    p = np.full((N, V), 1.0, dtype=np.float32)
+    p[:, 0] = 1000.0
+    p /= p.sum(axis=1, keepdims=True)
+    sym = np.zeros(N, dtype=np.int32)
+    cdf = krunch_ac.probs_to_cdf(p)
+    bits = krunch_ac.encode(cdf, sym)
+    assert len(bits) < N // 4, len(bits)
+    assert bits == orc.encode(cdf, sym)
+    np.testing.assert_array_equal(krunch_ac.decode(bits, cdf), sym)

@@ -62,6 +62,29 @@ def test_split_batches_are_byte_identical(eng, monkeypatch):
         np.testing.assert_array_equal(d, t)
 
 
+def test_calls_split_by_coder_bytes(eng):
+    """A small per-call coder-byte cap forces compress and decompress to run
+    as several calls (the path that keeps int32 stream offsets and the
+    uint32 buffer length of the C ABI in range on very large jobs): payloads
+    and tokens are the same as in one call."""
+    toks = [synthetic.zipf_tokens(1, 40 + 13 * i, seed_base=2100 + i)[0] for i in range(6)]
+    whole = eng.compress_tokens_batched(toks)
+    saved = eng.max_call_bytes
+    try:
+        # 2 streams of the longest (105 tokens: 484 coder bytes) per compress call
+        eng.max_call_bytes = 1000
+        split = eng.compress_tokens_batched(toks)
+        assert split == whole
+        eng.max_call_bytes = max(len(e) for e in whole) + 1      # one stream per decode call
+        for t, d in zip(toks, eng.decompress_tokens_batched(whole)):
+            np.testing.assert_array_equal(d, t)
+        eng.max_call_bytes = 10
+        with pytest.raises(ValueError):
+            eng.compress_tokens_batched(toks[:1])
+    finally:
+        eng.max_call_bytes = saved
+
+
 def test_decode_groups_and_graph_agree(eng):
     """Concurrent decode groups (graph branches) and the eager path decode the
     same tokens as one group."""
