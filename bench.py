@@ -40,7 +40,8 @@ def parse():
     ap.add_argument("--batch", type=int, default=256)
     ap.add_argument("--window", type=int, default=1024)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-decode-steps", type=int, default=48)
+    ap.add_argument("--cpu-decode-steps", type=int, default=1024,
+                    help="CPU baseline: tokens decoded (all of the window by default)")
     ap.add_argument("--head-rows", type=int, default=4096,
                     help="compress: rows per head GEMM + CDF block (the logits buffer holds this many rows)")
     ap.add_argument("--groups", type=int, default=1,
@@ -339,39 +340,27 @@ def dominant_kernel_roofline(weights16, B):
             "alg_bytes_per_launch": alg_bytes, "avg_launch_us": round(avg_s * 1e6, 3)}
 
 
-def cpu_baseline(weights16, args):
-    """The oracle (fp32 torch forward, numpy CDF, C range coder) on the host."""
+def cpu_baseline(args):
+    """BASELINE config 1 on the host cores: the oracle codec (oracle/codec.py:
+    fp32 row-wise torch forward, numpy CDF, C range coder) on the 169M-shaped
+    fp32 model (seed 0), one chunk of `window` Zipf(1.1) tokens: packed
+    compress, then stepped decompress of the first `cpu_decode_steps` tokens
+    (all of them by default), checked byte-exact."""
     import numpy as np
     import torch
     from krunch_amd import synthetic
-    from oracle import crc, rwkv4
-    from oracle import softmax as osm
+    from oracle import codec
 
     torch.set_num_threads(os.cpu_count() or 1)
-    w = {k: v.float() for k, v in weights16.items()}
+    w = synthetic.make_weights(dtype=torch.float32)
     T = args.window
-    toks = synthetic.zipf_tokens(1, T, repeat_rate=0.05)
-    inp = synthetic.model_inputs(toks)
+    toks = synthetic.zipf_tokens(1, T, repeat_rate=0.05)[0]
     t0 = time.perf_counter()
-    st = rwkv4.new_state(12, 1, 768)
-    lg = rwkv4.forward(w, torch.as_tensor(inp), st)[0].numpy()
-    cdf = osm.logits_to_cdf(lg)
-    lo, hi = osm.sym_intervals(cdf, toks[0])
-    bits = crc.encode_intervals(lo, hi)
+    bits, c_split = codec.compress(w, toks)
     t_c = time.perf_counter() - t0
     n_dec = min(args.cpu_decode_steps, T)
     t0 = time.perf_counter()
-    st = rwkv4.new_state(12, 1, 768)
-    dec = crc.Decoder(bits)
-    last, got = 0, []
-    for _ in range(n_dec):
-        row = rwkv4.forward(w, torch.tensor([[last]]), st)[0]
-        c = osm.logits_to_cdf(row.numpy())[0]
-        t = dec.target()
-        sym = int(np.searchsorted(c, t, side="right") - 1)
-        dec.consume(int(c[sym]), int(c[sym + 1]))
-        got.append(sym)
-        last = sym
+    got, d_split = codec.decompress(w, bits, n_dec)
     t_d = time.perf_counter() - t0
     c_tok_s, d_tok_s = T / t_c, n_dec / t_d
     rt = 1.0 / (1.0 / c_tok_s + 1.0 / d_tok_s)
@@ -385,10 +374,13 @@ def cpu_baseline(weights16, args):
         pass
     return {"value": round(rt * BYTES_PER_TOKEN / 1024, 3), "unit": "KB/s",
             "cores": torch.get_num_threads(), "kind": "port",
-            "sample": f"1 chunk: packed compress of {T} tokens + {n_dec} stepped decode steps "
-                      f"(fp32 torch forward, numpy CDF, C range coder)",
+            "sample": f"BASELINE config 1: 1 chunk, packed compress of {T} tokens + stepped "
+                      f"decompress of {n_dec} (fp32 row-wise torch forward with a fixed-order "
+                      f"C GEMM, numpy CDF, C range coder)",
             "compress_tok_s": round(c_tok_s, 1), "decompress_tok_s": round(d_tok_s, 2),
-            "cpu_packed_stepped_bit_identical": bool(np.array_equal(np.array(got), toks[0, :n_dec])),
+            "compress_split_s": {k: round(v, 3) for k, v in c_split.items()},
+            "decompress_split_s": {k: round(v, 3) for k, v in d_split.items()},
+            "cpu_packed_stepped_bit_identical": bool(np.array_equal(got, toks[:n_dec])),
             "cpu_model": cpu_model}
 
 
@@ -454,7 +446,7 @@ def main():
         }
     res["roofline"] = dominant_kernel_roofline(weights16, args.batch)
     if not args.no_cpu_baseline:
-        res["cpu_baseline"] = cpu_baseline(weights16, args)
+        res["cpu_baseline"] = cpu_baseline(args)
     print(json.dumps(res))
 
 

@@ -3,7 +3,10 @@
 The C range coder (oracle/range_coder.c) restates krunch_ac/cpu_reference.py
 and is pinned against oracle/range_coder.py in tests/test_oracle_rc.py. The
 same library holds the softmax's exp (oracle/softmax_kexp.c), used by
-oracle/softmax.py and pinned in tests/test_oracle_softmax.py.
+oracle/softmax.py and pinned in tests/test_oracle_softmax.py, and the
+fixed-order float32 GEMM of the row-wise forward (oracle/rowgemm.c), pinned in
+tests/test_oracle_rwkv.py against a float64 product and by its row
+invariance.
 """
 from __future__ import annotations
 
@@ -33,6 +36,9 @@ def lib():
         L.orc_decode_rows.argtypes = [P, P, ctypes.c_size_t, ctypes.c_uint32, ctypes.c_int, P]
         L.orc_kexp.argtypes = [P, P, ctypes.c_size_t]
         L.orc_kexp.restype = None
+        I = ctypes.c_int
+        L.orc_gemm_rows.argtypes = [P, I, I, P, I, P]
+        L.orc_gemm_rows.restype = None
         _LIB = L
     return _LIB
 
@@ -69,3 +75,17 @@ class Decoder:
         lib().orc_decode_rows(self._st, cdf.ctypes.data, cdf.shape[0], cdf.shape[1] - 1,
                               self.log2_total, out.ctypes.data)
         return out
+
+
+def gemm_rows(x: np.ndarray, W: np.ndarray) -> np.ndarray:
+    """float32 x [M, K] @ W [K, N], each output summed over k in order
+    (oracle/rowgemm.c): a row's result does not depend on M."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    W = np.ascontiguousarray(W, dtype=np.float32)
+    M, K = x.shape
+    assert W.shape[0] == K
+    N = W.shape[1]
+    y = np.empty((M, N), dtype=np.float32)
+    if M and N:
+        lib().orc_gemm_rows(x.ctypes.data, M, K, W.ctypes.data, N, y.ctypes.data)
+    return y

@@ -1,8 +1,9 @@
 """The w8a8 codec end to end on the GPU: logits against
-the fp32 oracle (north_star: 5e-2 max-abs) and against the oracle's own int8
-restatement; packed == stepped bit for bit (the CDFs of compress and
-decompress must agree); a byte-exact round trip and its bits/token beside the
-fp16 codec's."""
+the oracle's int8 restatement quantising the same fp16 activations
+(oracle.rwkv4.forward(w8a8=True, fp16=True)); the scheme's deviation from
+the fp32 oracle, an open deviation from north_star's 5e-2; packed == stepped
+bit for bit (the CDFs of compress and decompress must agree); a byte-exact
+round trip and its bits/token beside the fp16 codec's."""
 import numpy as np
 import pytest
 import torch
@@ -20,25 +21,45 @@ def model():
     return w16, cpp_path.init_weights(w16, "cuda", w8a8=True)
 
 
-def test_w8a8_logits_vs_fp32_oracle(model):
-    """Against the unquantised fp32 oracle the deviation is the quantisation
-    scheme's own: the oracle's int8 restatement (oracle/quant.py) is itself
-    0.135 max-abs / 0.020 mean-abs from fp32 on these random-init weights,
-    above north_star's 5e-2 max. The int8 noise is also chaotic: rounding the
-    oracle's activations to fp16 before quantising (as the GPU stores them)
-    moves its logits by 0.119 max / 0.018 mean. So the kernels are pinned
-    exactly where exactness is defined (tests/test_gpu_int8.py: quantisation
-    and integer GEMM bit for bit; packed == stepped below) and the model here
-    is held to the scheme's error: mean < 5e-2, max < 0.2."""
+def _gpu_and_oracles(model, B=2, T=24):
     w16, W = model
-    toks = synthetic.zipf_tokens(2, 24)
-    inp = synthetic.model_inputs(toks)
-    st = cpp_path.fresh_state_batched(W, 2)
-    got = cpp_path.forward_packed_batched(W, inp, st).float().cpu().numpy().reshape(2, 24, -1)
-    ref = rwkv4.forward(w16, torch.as_tensor(inp), rwkv4.new_state(12, 2, 768)).numpy()
-    d = np.abs(got - ref)
-    assert d.mean() < 5e-2, f"int8 logits vs fp32 oracle: mean abs {d.mean()}"
-    assert d.max() < 0.2, f"int8 logits vs fp32 oracle: max abs {d.max()}"
+    inp = synthetic.model_inputs(synthetic.zipf_tokens(B, T))
+    st = cpp_path.fresh_state_batched(W, B)
+    got = cpp_path.forward_packed_batched(W, inp, st).float().cpu().numpy().reshape(B, T, -1)
+    ids = torch.as_tensor(inp)
+    q16 = rwkv4.forward(w16, ids, rwkv4.new_state(12, B, 768), w8a8=True, fp16=True).numpy()
+    f32 = rwkv4.forward(w16, ids, rwkv4.new_state(12, B, 768)).numpy()
+    return got, q16, f32
+
+
+def test_w8a8_logits_vs_int8_oracle(model):
+    """The GPU int8 forward against the oracle's int8 restatement fed the
+    same fp16-rounded activations: within north_star's fp16 tolerance (1e-2;
+    measured 0.006 max / 6e-5 mean on MI355X). The two differ only where an
+    fp32 rounding difference upstream (GEMM order, exp, LayerNorm) flips an
+    fp16 activation and so an int8 step."""
+    got, q16, _ = _gpu_and_oracles(model)
+    d = np.abs(got - q16)
+    assert d.max() < 1e-2, f"int8 logits vs int8 oracle: max abs {d.max()}"
+    assert d.mean() < 1e-3, f"int8 logits vs int8 oracle: mean abs {d.mean()}"
+
+
+def test_w8a8_deviation_from_fp32_is_the_schemes(model):
+    """OPEN DEVIATION from north_star (int8 logits within 5e-2 of fp32): the
+    prescribed scheme (per-output-channel int8 weights, per-token dynamic
+    int8 activations) is itself 0.135 max-abs / 0.020 mean-abs from the fp32
+    oracle on these random-init weights, in exact arithmetic (the oracle
+    without fp16 rounding) as in the GPU's arithmetic. The GPU logits are
+    held to that scheme error: max < 0.2, mean < 5e-2 from fp32, and no
+    further from fp32 than the int8 oracle plus 1e-2."""
+    got, q16, f32 = _gpu_and_oracles(model)
+    d = np.abs(got - f32)
+    scheme = np.abs(q16 - f32).max()
+    msg = (f"int8 vs fp32: GPU max {d.max():.4f} mean {d.mean():.4f}; the scheme itself "
+           f"(int8 oracle) max {scheme:.4f} (open deviation: north_star asks 5e-2)")
+    assert d.mean() < 5e-2, msg
+    assert d.max() < 0.2, msg
+    assert d.max() < scheme + 1e-2, msg
 
 
 @pytest.mark.parametrize("B,T", [(3, 40), (2, 600)])

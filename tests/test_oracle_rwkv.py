@@ -55,3 +55,43 @@ def test_packed_equals_stepped_rowwise_and_windowed():
     windowed = torch.cat([rwkv4.forward(w, ids[:, :3], st_w, rowwise=True),
                           rwkv4.forward(w, ids[:, 3:], st_w, rowwise=True)], dim=1)
     assert torch.equal(packed, windowed)
+
+
+def test_fp16_rounding_points():
+    """forward(fp16=True) rounds activations where the production layer
+    stores fp16: its residual stream and logits are fp16-representable, it
+    stays within the fp16 tolerance of the fp32 forward, and the int8 codec
+    in that mode quantises rows of fp16 values."""
+    from krunch_amd import synthetic
+    w = synthetic.make_weights(n_layer=2, C=256, F=512, V=1000)
+    ids = torch.as_tensor(synthetic.model_inputs(synthetic.zipf_tokens(2, 12, V=1000)))
+    st = rwkv4.new_state(2, 2, 256)
+    f16 = rwkv4.forward(w, ids, st, fp16=True)
+    assert torch.equal(f16, f16.half().float())
+    for s in st:
+        assert torch.equal(s["att_xx"], s["att_xx"].half().float())
+    f32 = rwkv4.forward(w, ids, rwkv4.new_state(2, 2, 256))
+    assert (f16 - f32).abs().max() < 1e-2
+    q16 = rwkv4.forward(w, ids, rwkv4.new_state(2, 2, 256), w8a8=True, fp16=True)
+    assert torch.equal(q16, q16.half().float()) and (q16 - f32).abs().max() < 0.2
+
+
+def test_rowgemm_order_and_row_invariance():
+    """oracle/rowgemm.c: each output is the float32 sum over k in order
+    (checked against that sum spelled out in numpy float32, bit for bit),
+    close to the float64 product, and a row's bits do not depend on which
+    rows share the call (ragged M, N not a multiple of the column block)."""
+    from oracle import crc
+    rng = np.random.default_rng(3)
+    M, K, N = 37, 96, 1000
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    W = (rng.standard_normal((K, N)) * 0.05).astype(np.float32)
+    y = crc.gemm_rows(x, W)
+    acc = np.zeros((M, N), np.float32)
+    for k in range(K):
+        acc = (acc + (x[:, k:k + 1] * W[k:k + 1, :]).astype(np.float32)).astype(np.float32)
+    np.testing.assert_array_equal(y, acc)
+    np.testing.assert_allclose(y, x.astype(np.float64) @ W.astype(np.float64), rtol=1e-5, atol=1e-5)
+    for i in (0, 8, 36):
+        np.testing.assert_array_equal(crc.gemm_rows(x[i:i + 1], W), y[i:i + 1])
+    np.testing.assert_array_equal(crc.gemm_rows(x[5:30], W), y[5:30])
