@@ -251,6 +251,21 @@ int kr_layer_step(const kr_layer_weights* L, int C, int F, void* x, int B, int T
                   void* att_xx, float* aa, float* bb, float* pp, void* ffn_xx, void* ws,
                   size_t ws_bytes, void* stream);
 
+/* kr_layer_step without a workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc). No counterpart in the reference. The
+ * workspace is a static device array of KR_NOALLOC_SCRATCH_BYTES per GPU,
+ * held until the process ends; nothing is allocated or freed. A call whose
+ * kr_forward_workspace_bytes(B*T, C, F) exceeds it fails (KR_EINVAL): at
+ * C = 768, F = 3072 that is B*T <= 1024 rows. Every call on one GPU shares
+ * the array, so calls that overlap on one GPU (other streams or threads)
+ * race; consecutive calls on one stream do not. Same kernels and bits as
+ * kr_layer_step. */
+#define KR_NOALLOC_SCRATCH_BYTES (32u << 20)
+int kr_layer_step_noalloc(const kr_layer_weights* L, int C, int F, void* x, int B, int T,
+                          void* att_xx, float* aa, float* bb, float* pp, void* ffn_xx,
+                          void* stream);
+
 /* Layer phase profiler; replaces the reference's KRUNCH_PHASE_PROFILE
  * profiler with read_phase_times / reset_phase_times (layer_cpp.cpp:111-157,
  * 825-836). When on, every kr_layer_step call (outside stream capture)

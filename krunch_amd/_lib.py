@@ -71,6 +71,8 @@ _SIGS = {
     "kr_state_init": ([P, I, I, I, P], I),
     "kr_forward_workspace_bytes": ([LL, I, I], SZ),
     "kr_layer_step": ([ctypes.POINTER(KrLayerWeights), I, I, P, I, I, P, P, P, P, P, P, SZ, P], I),
+    "kr_layer_step_noalloc": ([ctypes.POINTER(KrLayerWeights), I, I, P, I, I, P, P, P, P, P, P],
+                              I),
     "kr_wkv": ([I, I, I, P, P, P, P, P, P, P, P, P, P], I),
     "kr_phase_profile": ([I], I),
     "kr_phase_count": ([], I),
@@ -124,6 +126,7 @@ def call(name: str, *args):
     return rc
 
 
+NOALLOC_SCRATCH_BYTES = 32 << 20      # KR_NOALLOC_SCRATCH_BYTES of include/krunch_hip.h
 U32_MAX = 0xFFFFFFFF
 I32_MAX = 0x7FFFFFFF
 

@@ -1072,6 +1072,36 @@ int profile_events() {
     return KR_OK;
 }
 
+// ---------------------------------------------------------------------------
+// Allocation-free layer step (kr_layer_step_noalloc): the workspace is this
+// file-scope device array, KR_NOALLOC_SCRATCH_BYTES per GPU, held until the
+// process ends. Host code never passes `scratch` itself (in host code the
+// name stands for a host-side shadow, not a device address): the device
+// address comes from hipGetSymbolAddress, once per device with that device
+// current, and only that address is handed to kernels.
+// ---------------------------------------------------------------------------
+static __device__ __align__(256) unsigned char scratch[KR_NOALLOC_SCRATCH_BYTES];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// The current device's address of `scratch` (looked up on first use there).
+int scratch_on_current_device(void** out) {
+    int dev = 0;
+    KR_HIP(hipGetDevice(&dev));
+    KR_REQUIRE(dev >= 0 && dev < kMaxDevices, "device %d out of range", dev);
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void* p = nullptr;
+        KR_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+        KR_REQUIRE(p != nullptr, "no device address for the static scratch on device %d", dev);
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return KR_OK;
+}
+
 }  // namespace
 
 // Entry points used by kr_engine.cpp.
@@ -1236,6 +1266,26 @@ int kr_layer_step(const kr_layer_weights* L, int C, int F, void* x, int B, int T
     }
     g_prof.calls++;
     return KR_OK;
+}
+
+int kr_layer_step_noalloc(const kr_layer_weights* L, int C, int F, void* x, int B, int T,
+                          void* att_xx, float* aa, float* bb, float* pp, void* ffn_xx,
+                          void* stream) {
+    KR_REQUIRE(L && x && att_xx && aa && bb && pp && ffn_xx,
+               "kr_layer_step_noalloc: null pointer");
+    KR_REQUIRE(C % 256 == 0 && C >= 256 && C <= 1024 && F % 64 == 0,
+               "kr_layer_step_noalloc: bad C/F");
+    KR_REQUIRE(B >= 1 && T >= 1, "kr_layer_step_noalloc: bad B=%d T=%d", B, T);
+    const long long M = (long long)B * T;
+    const size_t need = work_bytes(M, C, F);
+    KR_REQUIRE(need <= (size_t)KR_NOALLOC_SCRATCH_BYTES,
+               "kr_layer_step_noalloc: %lld rows need %zu workspace bytes, more than the "
+               "%zu-byte static scratch (use kr_layer_step with a workspace)",
+               M, need, (size_t)KR_NOALLOC_SCRATCH_BYTES);
+    void* ws = nullptr;
+    KR_TRY(scratch_on_current_device(&ws));
+    kr_layer_state st{att_xx, aa, bb, pp, ffn_xx};
+    return layer_forward(*L, C, F, Hm(x), B, T, st, carve(ws, M, C, F), kr_stream(stream));
 }
 
 int kr_phase_profile(int enable) {
