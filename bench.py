@@ -48,6 +48,9 @@ def parse():
                     help="decode the B streams as this many concurrent groups (graph branches)")
     ap.add_argument("--no-w8a8", action="store_true",
                     help="skip the w8a8 codec (BASELINE config 4) run on the same windows")
+    ap.add_argument("--hbm-table", metavar="CSV",
+                    help="print the per-kernel HBM fraction of a decode step from a rocprofv3 "
+                         "kernel-trace CSV of this bench (no GPU work)")
     ap.add_argument("--kernel-probe", action="store_true",
                     help="only run a 256 MiB device copy (counter calibration), 8 launches of "
                          "the dominant kernel and 2 eager launches of each other hot kernel at "
@@ -80,6 +83,20 @@ def kernel_probe(weights16, B):
         _lib.call("kr_det_matmul_packed", Af.data_ptr(), M, K, Wf.data_ptr(), N, out.data_ptr(), N,
                   5, res.data_ptr(), gate.data_ptr(), 0, _lib.stream_ptr())
     torch.cuda.synchronize()
+    # 8 launches of the channel-mix R + K products (one launch, as the step runs them)
+    xr = _pack(torch.rand((M, N), device=dev).half())
+    xk = _pack(torch.rand((M, N), device=dev).half())
+    rf = torch.empty((M, N), dtype=torch.float16, device=dev)
+    kf = torch.empty(_lib.lib().kr_fragment_bytes(M, K) // 2, dtype=torch.float16, device=dev)
+    jobs = (_lib.KrPackedJob * 2)()
+    jobs[0] = _lib.KrPackedJob(xr.data_ptr(), P.tensors["0.fRf"].data_ptr(), N, rf.data_ptr(), N,
+                               2, None, None, 0)
+    jobs[1] = _lib.KrPackedJob(xk.data_ptr(), P.tensors["0.fKf"].data_ptr(), K, kf.data_ptr(), K,
+                               3, None, None, 1)
+    for _ in range(8):
+        _lib.call("kr_det_matmul_packed_multi", jobs, 2, M, N, _lib.stream_ptr())
+    torch.cuda.synchronize()
+    del xr, xk, rf, kf
     del A, Af, res, gate, out
     s = _lib.stream_ptr()
     # one stepped layer (LN-mix, K/V/R+WKV, output projection, LN-mix, ffn R/K, ffn V) at B rows
@@ -262,59 +279,28 @@ def gpu_bench(args, weights16, w8a8=False):
     return dict(t_c=t_c, t_d=t_d, ntok=ntok, comp_bytes=comp_bytes, total_tok=B * L, exact=exact)
 
 
-def dominant_kernel_roofline(weights16, B):
-    """Live roofline of the dominant kernel of the timed region: the stepped
-    channel-mix value GEMM (M = B rows, K = 3072, N = 768, gated-residual
-    epilogue; the small-M MFMA kernel on fragment-packed operands, exactly as
-    the decode step launches it), 12 launches per decode step.
-
-    It is HBM-bound: algorithmic bytes per launch = W (K*N*2) + A (M*K*2) +
-    residual, gate and output (3*M*N*2). The average launch duration is
-    measured with HIP events on the launching stream around a captured graph
-    of back-to-back launches (graph replay keeps host launch cost out). As in
-    a decode step, where the other 256 MB of weights stream between two uses
-    of one layer's matrix, every launch reads a different weight copy (64
-    copies, 302 MB > the 256 MB Infinity Cache), so W comes from HBM.
-    `traffic` is read from the committed counter summary
-    profiles/gemm_panel_ffn_value_B256_traffic.json (rocprofv3 --pmc
-    FETCH_SIZE / WRITE_SIZE, scaled by a 256 MiB copy calibration)."""
+def _pack(X):
+    """Fragment-packed copy of a [R, K] fp16 device matrix (kr_pack_fragments)."""
     import torch
-    from krunch_amd import _lib, cpp_path
+    from krunch_amd import _lib
+    R, K = X.shape
+    buf = torch.empty(_lib.lib().kr_fragment_bytes(R, K) // 2, dtype=torch.float16,
+                      device=X.device)
+    _lib.call("kr_pack_fragments", X.data_ptr(), K, R, K, buf.data_ptr(), _lib.stream_ptr())
+    return buf
 
-    W = cpp_path.init_weights(weights16, "cuda")
-    P = W["prepared"]
-    K, N, M = P.F, P.C, B
-    dev = torch.device("cuda")
-    g = torch.Generator(device="cpu").manual_seed(3)
-    A = torch.rand((M, K), generator=g).half().to(dev)
-    res = torch.randn((M, N), generator=g).half().to(dev)
-    gate = torch.rand((M, N), generator=g).half().to(dev)
-    out = torch.empty((M, N), dtype=torch.float16, device=dev)
-    n_launch = 64
 
-    def packed(X):
-        R = X.shape[0]
-        buf = torch.empty(_lib.lib().kr_fragment_bytes(R, K) // 2, dtype=torch.float16, device=dev)
-        _lib.call("kr_pack_fragments", X.data_ptr(), K, R, K, buf.data_ptr(), _lib.stream_ptr())
-        return buf
-
-    Af = packed(A)
-    Wfs = [packed((torch.rand((N, K), generator=g) * 0.04 - 0.02).half().to(dev))
-           for _ in range(n_launch)]
-
-    def launches():
-        s = _lib.stream_ptr()
-        for i in range(n_launch):
-            _lib.call("kr_det_matmul_packed", Af.data_ptr(), M, K, Wfs[i].data_ptr(), N,
-                      out.data_ptr(), N, 5, res.data_ptr(), gate.data_ptr(), 0, s)
-
-    launches()
+def _graph_launch_us(launches):
+    """Average duration of one launch: a captured graph of n launches, timed
+    with HIP events on the stream it replays on (host launch cost kept out)."""
+    import torch
+    n = launches(None)
     torch.cuda.synchronize()
     graph = torch.cuda.CUDAGraph()
     stream = torch.cuda.Stream()
     with torch.cuda.stream(stream):
         with torch.cuda.graph(graph, stream=stream):
-            launches()
+            launches(stream)
     ms = []
     with torch.cuda.stream(stream):
         for _ in range(4):
@@ -325,19 +311,159 @@ def dominant_kernel_roofline(weights16, B):
             e1.record(stream)
             e1.synchronize()
             ms.append(e0.elapsed_time(e1))
-    avg_s = min(ms[1:]) / 1000.0 / n_launch
-    alg_bytes = K * N * 2 + M * K * 2 + 3 * M * N * 2
-    achieved = alg_bytes / avg_s / 1e9
+    return min(ms[1:]) * 1000.0 / n
+
+
+def _roofline_entry(kernel, alg_bytes, us, traffic_file, B):
     traffic = None
-    tfile = os.path.join(ROOT, "profiles", "gemm_panel_ffn_value_B256_traffic.json")
-    if os.path.exists(tfile) and M == 256:
+    tfile = os.path.join(ROOT, "profiles", traffic_file)
+    if os.path.exists(tfile) and B == 256:
         with open(tfile) as f:
             traffic = json.load(f).get("hbm_bytes_per_launch")
-    return {"kernel": "gemm_panel_kernel<2,2,frag> (stepped ffn value GEMM, M=%d K=%d N=%d, gated epilogue)"
-                      % (M, K, N),
-            "bound": "hbm", "achieved": round(achieved, 2), "peak": MI355X_HBM_PEAK / 1e9,
-            "unit": "GB/s", "frac": round(achieved / (MI355X_HBM_PEAK / 1e9), 4), "traffic": traffic,
-            "alg_bytes_per_launch": alg_bytes, "avg_launch_us": round(avg_s * 1e6, 3)}
+    achieved = alg_bytes / (us * 1e-6) / 1e9
+    return {"kernel": kernel, "bound": "hbm", "achieved": round(achieved, 2),
+            "peak": MI355X_HBM_PEAK / 1e9, "unit": "GB/s",
+            "frac": round(achieved / (MI355X_HBM_PEAK / 1e9), 4), "traffic": traffic,
+            "alg_bytes_per_launch": alg_bytes, "avg_launch_us": round(us, 3)}
+
+
+def dominant_kernel_roofline(weights16, B):
+    """Live rooflines of the two heaviest kernels of the timed region, both
+    stepped small-M products of the decode step (12 launches each per step),
+    HBM-bound:
+      * the channel-mix R and K products in one launch (M = B, K = 768,
+        N = 768 sigmoid + 3072 relu^2; the top kernel by time), algorithmic
+        bytes = W (768 + 3072) * 768 * 2 + A 2 * B * 768 * 2 + outputs
+        B * (768 + 3072) * 2;
+      * the channel-mix value product (M = B, K = 3072, N = 768, gated
+        residual), W 3072 * 768 * 2 + A B * 3072 * 2 + residual, gate and
+        output 3 * B * 768 * 2.
+    Each is launched exactly as the decode step launches it (fragment-packed
+    operands), in a captured graph of 64 launches over 64 distinct weight
+    copies (> the 256 MB memory-side cache, so weights come from HBM as in a
+    real step), timed with HIP events on the replay stream. `traffic` is the
+    HBM bytes per launch from the committed counter summaries
+    (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE on bench.py --kernel-probe,
+    scaled by a 256 MiB copy calibration)."""
+    import torch
+    from krunch_amd import _lib
+
+    dev = torch.device("cuda")
+    C, F, M = 768, 3072, B
+    g = torch.Generator(device="cpu").manual_seed(3)
+    n = 64
+    rnd = lambda *sh: (torch.rand(sh, generator=g) * 0.04 - 0.02).half().to(dev)
+
+    # channel-mix R + K in one launch
+    xr, xk = _pack(torch.rand((M, C), generator=g).half().to(dev)), \
+        _pack(torch.rand((M, C), generator=g).half().to(dev))
+    rf = torch.empty((M, C), dtype=torch.float16, device=dev)
+    kf = torch.empty(_lib.lib().kr_fragment_bytes(M, F) // 2, dtype=torch.float16, device=dev)
+    WR = [_pack(rnd(C, C)) for _ in range(n)]
+    WK = [_pack(rnd(F, C)) for _ in range(n)]
+    jobs = []
+    for i in range(n):
+        j = (_lib.KrPackedJob * 2)()
+        j[0] = _lib.KrPackedJob(xr.data_ptr(), WR[i].data_ptr(), C, rf.data_ptr(), C, 2, None, None, 0)
+        j[1] = _lib.KrPackedJob(xk.data_ptr(), WK[i].data_ptr(), F, kf.data_ptr(), F, 3, None, None, 1)
+        jobs.append(j)
+
+    def rk(stream):
+        s = _lib.stream_ptr(stream)
+        for i in range(n):
+            _lib.call("kr_det_matmul_packed_multi", jobs[i], 2, M, C, s)
+        return n
+
+    us_rk = _graph_launch_us(rk)
+    del WR, WK
+    bytes_rk = (C + F) * C * 2 + 2 * M * C * 2 + M * (C + F) * 2
+
+    # channel-mix value product
+    A = _pack(torch.rand((M, F), generator=g).half().to(dev))
+    res = torch.randn((M, C), generator=g).half().to(dev)
+    gate = torch.rand((M, C), generator=g).half().to(dev)
+    out = torch.empty((M, C), dtype=torch.float16, device=dev)
+    WV = [_pack(rnd(C, F)) for _ in range(n)]
+
+    def fv(stream):
+        s = _lib.stream_ptr(stream)
+        for i in range(n):
+            _lib.call("kr_det_matmul_packed", A.data_ptr(), M, F, WV[i].data_ptr(), C,
+                      out.data_ptr(), C, 5, res.data_ptr(), gate.data_ptr(), 0, s)
+        return n
+
+    us_v = _graph_launch_us(fv)
+    del WV
+    bytes_v = F * C * 2 + M * F * 2 + 3 * M * C * 2
+    top = _roofline_entry(
+        "gemm_panel_kernel<4,2,frag,256> (stepped channel-mix R + K products in one launch, "
+        "M=%d K=768 N=768 sigmoid + 3072 relu^2; top kernel by time)" % M,
+        bytes_rk, us_rk, "gemm_panel_ffn_rk_B256_traffic.json", B)
+    second = _roofline_entry(
+        "gemm_panel_kernel<2,2,frag,768> (stepped channel-mix value product, M=%d K=3072 N=768, "
+        "gated residual; second by time)" % M,
+        bytes_v, us_v, "gemm_panel_ffn_value_B256_traffic.json", B)
+    return top, second
+
+
+# Algorithmic bytes of each kernel of one stepped decode step (B streams,
+# C = 768, F = 3072, V = 50277, fp16 activations and weights, fp32 WKV
+# state), keyed by a substring of the kernel name; see DESIGN.md.
+def step_kernel_bytes(B, C=768, F=3072, V=50277):
+    h = 2
+    return [
+        ("ln_mix_kernel<3, 3>", "LN1 + 3 mixes", 12,
+         6 * B * C * h + 5 * C * h),
+        ("kvr_wkv_kernel", "K, V, R products + WKV", 12,
+         3 * C * C * h + 3 * B * C * h + 2 * C * 4 + 2 * 3 * B * C * 4 + B * C * h),
+        ("gemm_panel_kernel<2, 2, true, 256", "output projection (residual)", 12,
+         C * C * h + 4 * B * C * h),
+        ("ln_mix_kernel<3, 2>", "LN2 + 2 mixes", 12,
+         5 * B * C * h + 4 * C * h),
+        ("gemm_panel_kernel<4, 2, true, 256", "channel-mix R + K products", 12,
+         (C + F) * C * h + 2 * B * C * h + B * (C + F) * h),
+        ("gemm_panel_kernel<2, 2, true, 768", "channel-mix value product (gated residual)", 12,
+         C * F * h + B * F * h + 3 * B * C * h),
+        ("ln_mix_kernel<3, 0>", "LN_out", 1,
+         2 * B * C * h + 2 * C * h),
+        ("gemm_head_small_kernel", "head (M = B, N = V)", 1,
+         V * C * h + B * C * h + B * V * h),
+        ("row_cdf_kernel<0, 4>", "softmax -> CDF -> range decode", 1,
+         B * V * h),
+    ]
+
+
+def hbm_table(csv_path, B):
+    """Per-kernel HBM fraction of one decode step from a rocprofv3 kernel
+    trace of the bench (markdown on stdout): each kernel's algorithmic bytes
+    per launch over its average duration in the trace's decode steps
+    (the most frequent grid of that kernel), against 8 TB/s."""
+    import csv
+    import gzip
+    opener = gzip.open if csv_path.endswith(".gz") else open
+    durs = {}
+    with opener(csv_path, "rt") as f:
+        for r in csv.DictReader(f):
+            key = (r["Kernel_Name"], int(r["Grid_Size_X"]))
+            durs.setdefault(key, []).append(
+                (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1000.0)
+    print(f"| kernel | phase | launches / step | avg us | algorithmic MB / launch | GB/s | "
+          f"fraction of 8 TB/s | us / step |")
+    print("|---|---|---|---|---|---|---|---|")
+    total = 0.0
+    for sub, phase, per_step, nbytes in step_kernel_bytes(B):
+        cands = [(len(v), k) for k, v in durs.items() if sub in k[0]]
+        if not cands:
+            continue
+        _, key = max(cands)
+        us = sorted(durs[key])[len(durs[key]) // 2]       # median launch
+        gbs = nbytes / (us * 1e-6) / 1e9
+        total += us * per_step
+        name = key[0].replace("(anonymous namespace)::", "").replace("void ", "").split("(")[0]
+        print(f"| `{name}` | {phase} | {per_step} | {us:.2f} | {nbytes / 1e6:.2f} | {gbs:.0f} | "
+              f"{gbs / (MI355X_HBM_PEAK / 1e9):.3f} | {us * per_step:.1f} |")
+    print(f"\nSum over the step: {total:.1f} us (median launches; the profiler adds ~1 us per "
+          f"kernel).")
 
 
 def cpu_baseline(args):
@@ -392,6 +518,9 @@ def main():
               "has no multi-GPU path (see DESIGN.md, 'How it would shard'). Run with --gpus 1.",
               file=sys.stderr)
         sys.exit(2)
+    if args.hbm_table:
+        hbm_table(args.hbm_table, args.batch)
+        return
     import torch
     from krunch_amd import synthetic
     weights16 = synthetic.make_weights()
@@ -444,7 +573,7 @@ def main():
             "roundtrip_exact": q["exact"],
             "compress_int8_fp16_tops": round(q["ntok"] * FLOP_PER_TOKEN / q["t_c"] / 1e12, 1),
         }
-    res["roofline"] = dominant_kernel_roofline(weights16, args.batch)
+    res["roofline"], res["roofline_second_kernel"] = dominant_kernel_roofline(weights16, args.batch)
     if not args.no_cpu_baseline:
         res["cpu_baseline"] = cpu_baseline(args)
     print(json.dumps(res))

@@ -171,6 +171,24 @@ int kr_det_matmul_packed(const uint16_t* xf, int M, int K, const uint16_t* Wf, i
                          long long ldo, int epilogue, const uint16_t* res, const uint16_t* gate,
                          int out_packed, void* stream);
 
+/* Up to three kr_det_matmul_packed products sharing M and K in one launch of
+ * the small-M kernel (independent outputs, same bits as separate calls): the
+ * stepped layer runs its channel-mix R (sigmoid) and K (relu^2, packed
+ * output) products this way. No reference counterpart: the reference runs
+ * them as two matmuls (layer_cpp.cpp:623-628). M <= 512. */
+typedef struct kr_packed_job {
+    const uint16_t* xf;          /* x [M, K] fragment-packed */
+    const uint16_t* Wf;          /* Wt [N, K] fragment-packed */
+    int N;
+    void* out;                   /* as kr_det_matmul_packed */
+    long long ldo;
+    int epilogue;
+    const uint16_t* res;
+    const uint16_t* gate;
+    int out_packed;
+} kr_packed_job;
+int kr_det_matmul_packed_multi(const kr_packed_job* jobs, int n_jobs, int M, int K, void* stream);
+
 /* w8a8 (the reference only sketches an int8 path,
  * docs/INT8_WEIGHTS_DESIGN.md): symmetric int8 with one fp32 scale per row,
  * s = max|x| / 127 (1 when the row is zero), q = clamp(rint(x / s), -127, 127).

@@ -18,6 +18,11 @@ U32 = ctypes.c_uint32
 SZ = ctypes.c_size_t
 
 
+class KrPackedJob(ctypes.Structure):
+    _fields_ = [("xf", P), ("Wf", P), ("N", I), ("out", P), ("ldo", LL), ("epilogue", I),
+                ("res", P), ("gate", P), ("out_packed", I)]
+
+
 class KrMatrixQ8(ctypes.Structure):
     _fields_ = [("q", P), ("qf", P), ("scale", P)]
 
@@ -63,6 +68,7 @@ _SIGS = {
     "kr_fragment_bytes": ([I, I], ctypes.c_size_t),
     "kr_pack_fragments": ([P, LL, I, I, P, P], I),
     "kr_det_matmul_packed": ([P, I, I, P, I, P, LL, I, P, P, I, P], I),
+    "kr_det_matmul_packed_multi": ([ctypes.POINTER(KrPackedJob), I, I, I, P], I),
     "kr_quant_bytes": ([I, I, I], ctypes.c_size_t),
     "kr_quantize_rows": ([P, LL, I, I, P, P, I, P], I),
     "kr_det_matmul_i8": ([P, P, I, I, P, P, I, P, LL, I, P, P, I, P], I),

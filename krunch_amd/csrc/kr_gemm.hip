@@ -22,6 +22,7 @@
 #include <type_traits>
 
 #include "kr_gemm.h"
+#include "krunch_hip.h"
 
 namespace {
 
@@ -1134,6 +1135,34 @@ int kr_det_matmul(const uint16_t* x, int M, int K, const uint16_t* Wt, long long
     g.N = N;
     g.K = K;
     return kr_gemm_launch(g, epilogue, kr_stream(stream));
+}
+
+int kr_det_matmul_packed_multi(const kr_packed_job* jobs, int n_jobs, int M, int K,
+                               void* stream) {
+    KR_REQUIRE(jobs && n_jobs >= 1 && n_jobs <= KR_GEMM_MAX_JOBS,
+               "kr_det_matmul_packed_multi: 1..%d jobs", KR_GEMM_MAX_JOBS);
+    KR_REQUIRE(M >= 0 && M <= KR_GEMM_SMALL_M && K > 0,
+               "kr_det_matmul_packed_multi: M=%d K=%d (M <= %d)", M, K, KR_GEMM_SMALL_M);
+    kr_gemm_args g[KR_GEMM_MAX_JOBS] = {};
+    int eps[KR_GEMM_MAX_JOBS] = {};
+    for (int j = 0; j < n_jobs; j++) {
+        const kr_packed_job& p = jobs[j];
+        KR_REQUIRE(p.xf && p.Wf && p.out, "kr_det_matmul_packed_multi: null pointer in job %d", j);
+        g[j].A = reinterpret_cast<const kr_half*>(p.xf);
+        g[j].lda = K;
+        g[j].Wf = reinterpret_cast<const kr_half*>(p.Wf);
+        g[j].out = p.out;
+        g[j].ldo = p.ldo;
+        g[j].res = reinterpret_cast<const kr_half*>(p.res);
+        g[j].gate = reinterpret_cast<const kr_half*>(p.gate);
+        g[j].M = M;
+        g[j].N = p.N;
+        g[j].K = K;
+        g[j].a_frag = 1;
+        g[j].out_frag = p.out_packed ? 1 : 0;
+        eps[j] = p.epilogue;
+    }
+    return kr_gemm_launch_multi(g, eps, n_jobs, kr_stream(stream));
 }
 
 int kr_det_matmul_packed(const uint16_t* xf, int M, int K, const uint16_t* Wf, int N, void* out,

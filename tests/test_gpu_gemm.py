@@ -110,3 +110,39 @@ def test_packed_operands_match_row_major(M, K, N, ep):
         _lib.call("kr_det_matmul_packed", xf.data_ptr(), M, K, Wf.data_ptr(), N, of.data_ptr(), N,
                   ep, None, None, 1, _lib.stream_ptr())
         assert torch.equal(of, pack(want))
+
+
+def test_packed_multi_equals_separate_launches():
+    """kr_det_matmul_packed_multi (the stepped channel-mix R and K products
+    in one launch: sigmoid into a row-major gate, relu^2 into a packed
+    operand) gives the bits of two kr_det_matmul_packed calls."""
+    from krunch_amd import _lib
+    M, K = 256, 768
+    g = torch.Generator(device="cpu").manual_seed(21)
+    x = torch.randn((M, K), generator=g).half().cuda()
+    WR = (torch.randn((768, K), generator=g) * 0.03).half().cuda()
+    WK = (torch.randn((3072, K), generator=g) * 0.03).half().cuda()
+
+    def pack(X):
+        R, KK = X.shape
+        buf = torch.empty(_lib.lib().kr_fragment_bytes(R, KK) // 2, dtype=torch.float16,
+                          device="cuda")
+        _lib.call("kr_pack_fragments", X.data_ptr(), KK, R, KK, buf.data_ptr(), _lib.stream_ptr())
+        return buf
+
+    xf, WRf, WKf = pack(x), pack(WR), pack(WK)
+    r1 = torch.empty((M, 768), dtype=torch.float16, device="cuda")
+    k1 = torch.zeros(_lib.lib().kr_fragment_bytes(M, 3072) // 2, dtype=torch.float16, device="cuda")
+    _lib.call("kr_det_matmul_packed", xf.data_ptr(), M, K, WRf.data_ptr(), 768, r1.data_ptr(), 768,
+              2, None, None, 0, _lib.stream_ptr())
+    _lib.call("kr_det_matmul_packed", xf.data_ptr(), M, K, WKf.data_ptr(), 3072, k1.data_ptr(),
+              3072, 3, None, None, 1, _lib.stream_ptr())
+    r2 = torch.empty_like(r1)
+    k2 = torch.zeros_like(k1)
+    jobs = (_lib.KrPackedJob * 2)()
+    jobs[0] = _lib.KrPackedJob(xf.data_ptr(), WRf.data_ptr(), 768, r2.data_ptr(), 768, 2, None,
+                               None, 0)
+    jobs[1] = _lib.KrPackedJob(xf.data_ptr(), WKf.data_ptr(), 3072, k2.data_ptr(), 3072, 3, None,
+                               None, 1)
+    _lib.call("kr_det_matmul_packed_multi", jobs, 2, M, K, _lib.stream_ptr())
+    assert torch.equal(r1, r2) and torch.equal(k1, k2)
