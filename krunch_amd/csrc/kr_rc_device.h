@@ -12,47 +12,60 @@
 // partial byte at the starting offset are kept (the buffer is zero-filled by
 // the caller, as in the reference's contract), completed bytes are stored
 // whole, writes at or past `cap` are dropped and counted in `overflow`.
+// Bits gather in a 64-bit accumulator (MSB first) and leave four bytes at a
+// time, so a run of n bits costs one or two shifts instead of n steps.
 struct kr_bit_sink {
     uint8_t* buf;
-    uint32_t byte;
-    uint32_t cur;
-    uint32_t nb;
+    uint32_t byte;      // index of the byte the accumulator's top byte goes to
+    uint64_t acc;       // pending bits, MSB-aligned
+    uint32_t nacc;      // number of pending bits (< 32 between calls)
     uint32_t cap;
     uint32_t overflow;
 
     __device__ void open(uint8_t* b, uint32_t bitpos, uint32_t capacity) {
         buf = b;
         byte = bitpos >> 3;
-        nb = bitpos & 7u;
+        nacc = bitpos & 7u;
         cap = capacity;
         overflow = 0;
-        cur = 0;
-        if (nb) cur = (byte < cap ? (uint32_t)buf[byte] : 0u) & ((0xFF00u >> nb) & 0xFFu);
-    }
-    __device__ void emit_byte() {
-        if (byte < cap) buf[byte] = (uint8_t)cur;
-        else overflow = 1;
-        byte++;
-        cur = 0;
-        nb = 0;
-    }
-    __device__ void put(uint32_t bit) {
-        cur |= bit << (7u - nb);
-        if (++nb == 8u) emit_byte();
-    }
-    __device__ void put_run(uint32_t bit, uint32_t n) {
-        while (n && nb) { put(bit); n--; }
-        const uint32_t fill = bit ? 0xFFu : 0u;
-        while (n >= 8u) { cur = fill; emit_byte(); n -= 8u; }
-        while (n) { put(bit); n--; }
-    }
-    // Stores the trailing partial byte; returns the new bit offset.
-    __device__ uint32_t close() {
-        if (nb) {
-            if (byte < cap) buf[byte] = (uint8_t)cur;
-            else overflow = 1;
+        acc = 0;
+        if (nacc) {
+            const uint32_t keep = (byte < cap ? (uint32_t)buf[byte] : 0u) & ((0xFF00u >> nacc) & 0xFFu);
+            acc = (uint64_t)keep << 56;
         }
-        return byte * 8u + nb;
+    }
+    __device__ void store_byte(uint32_t idx, uint32_t v) {
+        if (idx < cap) buf[idx] = (uint8_t)v;
+        else overflow = 1;
+    }
+    // Append the n low bits of v, most significant first (1 <= n <= 32).
+    __device__ void put_bits(uint32_t v, uint32_t n) {
+        acc |= (uint64_t)v << (64u - nacc - n);
+        nacc += n;
+        if (nacc >= 32u) {
+            #pragma unroll
+            for (uint32_t i = 0; i < 4u; i++) store_byte(byte + i, (uint32_t)(acc >> (56u - 8u * i)) & 0xFFu);
+            byte += 4u;
+            acc <<= 32;
+            nacc -= 32u;
+        }
+    }
+    __device__ void put(uint32_t bit) { put_bits(bit, 1u); }
+    // n copies of `bit` (any n).
+    __device__ void put_run(uint32_t bit, uint32_t n) {
+        while (n >= 32u) { put_bits(bit ? 0xFFFFFFFFu : 0u, 32u); n -= 32u; }
+        if (n) put_bits(bit ? (1u << n) - 1u : 0u, n);
+    }
+    // Stores the remaining bytes (the last one partial); returns the new bit offset.
+    __device__ uint32_t close() {
+        while (nacc >= 8u) {
+            store_byte(byte, (uint32_t)(acc >> 56));
+            acc <<= 8;
+            nacc -= 8u;
+            byte++;
+        }
+        if (nacc) store_byte(byte, (uint32_t)(acc >> 56));
+        return byte * 8u + nacc;
     }
 };
 
@@ -67,6 +80,12 @@ struct kr_bit_source {
         const uint32_t bit = (b >> (7u - (pos & 7u))) & 1u;
         pos++;
         return bit;
+    }
+    // The next n bits as an integer, first bit most significant (n <= 31).
+    __device__ uint32_t get_bits(uint32_t n) {
+        uint32_t v = 0;
+        for (uint32_t i = 0; i < n; i++) v = (v << 1) | get();
+        return v;
     }
 };
 
@@ -114,6 +133,19 @@ struct kr_bit_window {
         pos++;
         return bit;
     }
+    // The next n bits as an integer, first bit most significant (n <= 31):
+    // one shift out of the window when it holds them, else bit by bit.
+    __device__ uint32_t get_bits(uint32_t n) {
+        if (n == 0u) return 0u;
+        const uint32_t off = pos - base;
+        if (off + n <= 64u) {
+            pos += n;
+            return (uint32_t)((w << off) >> (64u - n));
+        }
+        uint32_t v = 0;
+        for (uint32_t i = 0; i < n; i++) v = (v << 1) | get();
+        return v;
+    }
 };
 
 // Narrow [low, high] to the symbol's cumulative range [c_lo, c_hi) of 2^prec.
@@ -126,30 +158,40 @@ __device__ __forceinline__ void kr_rc_narrow(uint32_t& low, uint32_t& high, uint
     high = nh;
 }
 
+// Renormalisation in closed form, the same bits and state as the spec's loop
+// (cpu_reference.py:91-147, one E1/E2/E3 step per iteration):
+//  * E1/E2 shift out the leading bits low and high share, n1 = clz(low ^ high)
+//    of them (the narrowed interval is >= 64 wide, so n1 <= 26). The first
+//    one is followed by the pending (E3) complements, the others by none.
+//  * Then low = 01..., high = 10... and E3 repeats while low holds 1 and high
+//    0 in the next bit down: k = the run of such positions from bit 30. Each
+//    E3 step maps x to 2 (x - 2^30) = (x << 1) ^ 2^31, so k steps give
+//    (x << k) ^ 2^31 (high also takes k one bits at the bottom). After an E3
+//    step low < 2^31 <= high again, so no E1/E2 step can follow.
+__device__ __forceinline__ uint32_t kr_rc_e3_run(uint32_t low, uint32_t high) {
+    const uint32_t k = __clz(((~low) | high) << 1);
+    return k > 30u ? 30u : k;
+}
+
 __device__ __forceinline__ void kr_rc_encode(uint32_t& low, uint32_t& high, uint32_t& pending,
                                              uint32_t c_lo, uint32_t c_hi, int prec,
                                              kr_bit_sink& sink) {
     kr_rc_narrow(low, high, c_lo, c_hi, prec);
-    for (;;) {
-        if (high < KR_RC_HALF) {
-            sink.put(0u);
-            sink.put_run(1u, pending);
-            pending = 0;
-            low <<= 1;
-            high = (high << 1) | 1u;
-        } else if (low >= KR_RC_HALF) {
-            sink.put(1u);
-            sink.put_run(0u, pending);
-            pending = 0;
-            low = (low - KR_RC_HALF) << 1;
-            high = ((high - KR_RC_HALF) << 1) | 1u;
-        } else if (low >= KR_RC_QUARTER && high < KR_RC_3QUARTER) {
-            pending++;
-            low = (low - KR_RC_QUARTER) << 1;
-            high = ((high - KR_RC_QUARTER) << 1) | 1u;
-        } else {
-            break;
-        }
+    const uint32_t n1 = __clz(low ^ high);
+    if (n1) {
+        const uint32_t b0 = low >> 31;
+        sink.put_bits(b0, 1u);
+        sink.put_run(b0 ^ 1u, pending);
+        pending = 0;
+        if (n1 > 1u) sink.put_bits((low >> (32u - n1)) & ((1u << (n1 - 1u)) - 1u), n1 - 1u);
+        low <<= n1;
+        high = (high << n1) | ((1u << n1) - 1u);
+    }
+    const uint32_t k = kr_rc_e3_run(low, high);
+    if (k) {
+        pending += k;
+        low = (low << k) ^ KR_RC_HALF;
+        high = ((high << k) ^ KR_RC_HALF) | ((1u << k) - 1u);
     }
 }
 
@@ -171,15 +213,19 @@ template <class Source>
 __device__ __forceinline__ void kr_rc_consume(uint32_t& low, uint32_t& high, uint32_t& value,
                                               uint32_t c_lo, uint32_t c_hi, int prec,
                                               Source& src) {
+    // the closed-form renormalisation of kr_rc_encode; value moves with low
+    // and takes the stream's next bits at the bottom (cpu_reference.py:214-234)
     kr_rc_narrow(low, high, c_lo, c_hi, prec);
-    for (;;) {
-        uint32_t shift;
-        if (high < KR_RC_HALF) shift = 0u;
-        else if (low >= KR_RC_HALF) shift = KR_RC_HALF;
-        else if (low >= KR_RC_QUARTER && high < KR_RC_3QUARTER) shift = KR_RC_QUARTER;
-        else break;
-        low = (low - shift) << 1;
-        high = ((high - shift) << 1) | 1u;
-        value = ((value - shift) << 1) | src.get();
+    const uint32_t n1 = __clz(low ^ high);
+    if (n1) {
+        low <<= n1;
+        high = (high << n1) | ((1u << n1) - 1u);
+        value = (value << n1) | src.get_bits(n1);
+    }
+    const uint32_t k = kr_rc_e3_run(low, high);
+    if (k) {
+        low = (low << k) ^ KR_RC_HALF;
+        high = ((high << k) ^ KR_RC_HALF) | ((1u << k) - 1u);
+        value = ((value << k) ^ KR_RC_HALF) | src.get_bits(k);
     }
 }
