@@ -420,16 +420,21 @@ __global__ void __launch_bounds__(256) wkv_kernel(const float* __restrict__ k,
 // the products run.
 // ---------------------------------------------------------------------------
 struct KvrWkvArgs {
-    const kr_half* A[3];       // mixes for K, V, R: fragment-packed [M16, C]
+    const kr_half* A[3];       // mixes for K, V, R: fragment-packed [M16, C] (int8: same bytes)
     const kr_half* Wf[3];      // K, V, R weights, W^T fragment-packed ([C, C])
+    const float* sa[3];        // w8a8: per-row scales of the three mixes
+    const float* sw[3];        // w8a8: per-output-channel scales of K, V, R
     const float* decay;        // [C] time decay (already -exp)
     const float* first;        // [C] time first
     float* aa;                 // [M, C] WKV state, updated in place
     float* bb;
     float* pp;
     kr_half* ry;               // fragment-packed [M16, C] (K = C operand of the output GEMM)
+                               // or, for w8a8, row-major [M, C] (the quantiser's input)
     int M;
 };
+
+__device__ __forceinline__ kr_int4 as_int4(kr_half8 v) { return __builtin_bit_cast(kr_int4, v); }
 
 // Asynchronous 16-byte copy global -> LDS (lane l writes lds_base + 16 l);
 // counted in vmcnt like a load, no VGPRs held.
@@ -439,10 +444,15 @@ __device__ __forceinline__ void lds_dma16(const void* src, void* lds_base) {
         (__attribute__((address_space(3))) void*)lds_base, 16, 0, 0);
 }
 
-template <int S, int TM, int NS>
+// I8 (w8a8): int8 operands in the same 1 KB block layout (a 16 x 64 int8
+// block is the 16 x 32 block of the 16-bit view), v_mfma_i32_16x16x64_i8,
+// the slice partials summed exactly in int32, then value = (float(acc) *
+// sa[m]) * sw[n], the int8 GEMM's dequantisation; ry is written row-major.
+template <int S, int TM, int NS, bool I8>
 __global__ void __launch_bounds__(192 * S) kvr_wkv_kernel(KvrWkvArgs a) {
     constexpr int C = 256 * S, NW = 3 * S, TT = TM * NS;
-    constexpr int KB = C / 32;                        // 1 KB blocks per fragment row
+    constexpr int KB = I8 ? C / 64 : C / 32;          // 1 KB blocks per fragment row
+    constexpr int QS = I8 ? 4 : 8;                    // blocks per 256-wide slice
     __shared__ __attribute__((aligned(16))) float part[3 * S * TT * 256];   // slice partials
     __shared__ __attribute__((aligned(16))) char wk[TT * 5 * 1024];         // WKV operands
 
@@ -469,22 +479,36 @@ __global__ void __launch_bounds__(192 * S) kvr_wkv_kernel(KvrWkvArgs a) {
     // ---- operands of product j over slice s, then the WKV operands into LDS
     const kr_half* Aj = j == 0 ? a.A[0] : (j == 1 ? a.A[1] : a.A[2]);
     const kr_half* Wf = j == 0 ? a.Wf[0] : (j == 1 ? a.Wf[1] : a.Wf[2]);
-    kr_half8 av[TM][8], b[NS][8];
+    kr_half8 av[TM][QS], b[NS][QS];
     #pragma unroll
     for (int i = 0; i < TM; i++) {
-        const kr_half* ap = Aj + ((size_t)min((m0 >> 4) + i, last_mb) * KB + 8 * s) * 512 + lane * 8;
+        const kr_half* ap = Aj + ((size_t)min((m0 >> 4) + i, last_mb) * KB + QS * s) * 512 + lane * 8;
         #pragma unroll
-        for (int q = 0; q < 8; q++) av[i][q] = *reinterpret_cast<const kr_half8*>(ap + 512 * q);
+        for (int q = 0; q < QS; q++) av[i][q] = *reinterpret_cast<const kr_half8*>(ap + 512 * q);
     }
     #pragma unroll
     for (int t = 0; t < NS; t++) {
-        const kr_half* bp = Wf + ((size_t)((n0 >> 4) + t) * KB + 8 * s) * 512 + lane * 8;
+        const kr_half* bp = Wf + ((size_t)((n0 >> 4) + t) * KB + QS * s) * 512 + lane * 8;
         #pragma unroll
-        for (int q = 0; q < 8; q++) b[t][q] = *reinterpret_cast<const kr_half8*>(bp + 512 * q);
+        for (int q = 0; q < QS; q++) b[t][q] = *reinterpret_cast<const kr_half8*>(bp + 512 * q);
     }
     // in tile t a lane owns row tile_m(t), columns tile_n(t) .. +3
     auto tile_m = [&](int t) { return m0 + 16 * (t / NS) + (lane & 15); };
     auto tile_n = [&](int t) { return n0 + 16 * (t % NS) + 4 * (lane >> 4); };
+    // w8a8 scales of this wave's tile (each wave folds at most one tile when
+    // TT <= NW; more tiles reload them in the loop below)
+    float q_sa[3] = {0.f, 0.f, 0.f};
+    kr_float4 q_sw[3] = {};
+    if constexpr (I8) {
+        if (wave < TT) {
+            const int qm = min(tile_m(wave), M - 1), qn = tile_n(wave);
+            #pragma unroll
+            for (int jj = 0; jj < 3; jj++) {
+                q_sa[jj] = a.sa[jj][qm];
+                q_sw[jj] = *reinterpret_cast<const kr_float4*>(a.sw[jj] + qn);
+            }
+        }
+    }
     for (int t = wave; t < TT; t += NW) {
         const int en = tile_n(t);
         const size_t o = (size_t)min(tile_m(t), M - 1) * C + en;
@@ -501,11 +525,21 @@ __global__ void __launch_bounds__(192 * S) kvr_wkv_kernel(KvrWkvArgs a) {
     for (int i = 0; i < TM; i++)
         #pragma unroll
         for (int t = 0; t < NS; t++) {
-            kr_float4 acc = kr_float4{0.f, 0.f, 0.f, 0.f};
-            #pragma unroll
-            for (int q = 0; q < 8; q++)
-                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(b[t][q], av[i][q], acc, 0, 0, 0);
-            *reinterpret_cast<kr_float4*>(part + ((j * S + s) * TT + i * NS + t) * 256 + lane * 4) = acc;
+            float* pd = part + ((j * S + s) * TT + i * NS + t) * 256 + lane * 4;
+            if constexpr (I8) {
+                kr_int4 acc = kr_int4{0, 0, 0, 0};
+                #pragma unroll
+                for (int q = 0; q < QS; q++)
+                    acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(as_int4(b[t][q]), as_int4(av[i][q]),
+                                                                acc, 0, 0, 0);
+                *reinterpret_cast<kr_int4*>(pd) = acc;
+            } else {
+                kr_float4 acc = kr_float4{0.f, 0.f, 0.f, 0.f};
+                #pragma unroll
+                for (int q = 0; q < QS; q++)
+                    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(b[t][q], av[i][q], acc, 0, 0, 0);
+                *reinterpret_cast<kr_float4*>(pd) = acc;
+            }
         }
     // the WKV copies of every wave must have landed before the barrier
     __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -516,11 +550,28 @@ __global__ void __launch_bounds__(192 * S) kvr_wkv_kernel(KvrWkvArgs a) {
         const int em = tile_m(t), en = tile_n(t);
         if (em >= M) continue;
         auto fold = [&](int jj) {
-            kr_float4 v = *reinterpret_cast<const kr_float4*>(part + (jj * S * TT + t) * 256 + lane * 4);
-            #pragma unroll
-            for (int q = 1; q < S; q++)
-                v = v + *reinterpret_cast<const kr_float4*>(part + ((jj * S + q) * TT + t) * 256 + lane * 4);
-            return v;
+            if constexpr (I8) {
+                kr_int4 iv = *reinterpret_cast<const kr_int4*>(part + (jj * S * TT + t) * 256 + lane * 4);
+                #pragma unroll
+                for (int q = 1; q < S; q++)
+                    iv = iv + *reinterpret_cast<const kr_int4*>(part + ((jj * S + q) * TT + t) * 256 + lane * 4);
+                float sa = q_sa[jj];
+                kr_float4 sw = q_sw[jj];
+                if (t != wave) {   // a second tile of this wave
+                    sa = a.sa[jj][tile_m(t)];
+                    sw = *reinterpret_cast<const kr_float4*>(a.sw[jj] + tile_n(t));
+                }
+                kr_float4 v;
+                #pragma unroll
+                for (int e = 0; e < 4; e++) v[e] = __fmul_rn(__fmul_rn((float)iv[e], sa), sw[e]);
+                return v;
+            } else {
+                kr_float4 v = *reinterpret_cast<const kr_float4*>(part + (jj * S * TT + t) * 256 + lane * 4);
+                #pragma unroll
+                for (int q = 1; q < S; q++)
+                    v = v + *reinterpret_cast<const kr_float4*>(part + ((jj * S + q) * TT + t) * 256 + lane * 4);
+                return v;
+            }
         };
         const kr_float4 k = fold(0), v = fold(1), rv = fold(2);
         const char* d = wk + t * 5 * 1024 + 16 * lane;
@@ -543,7 +594,8 @@ __global__ void __launch_bounds__(192 * S) kvr_wkv_kernel(KvrWkvArgs a) {
         *reinterpret_cast<kr_float4*>(a.aa + o) = sa;
         *reinterpret_cast<kr_float4*>(a.bb + o) = sb;
         *reinterpret_cast<kr_float4*>(a.pp + o) = sp;
-        *reinterpret_cast<kr_half4*>(a.ry + kr_frag_index(em, en, C)) = ry;
+        if constexpr (I8) *reinterpret_cast<kr_half4*>(a.ry + o) = ry;
+        else *reinterpret_cast<kr_half4*>(a.ry + kr_frag_index(em, en, C)) = ry;
     }
 }
 
@@ -617,11 +669,11 @@ int launch_ln_mix(int G, const LnMixArgs& a_in, hipStream_t s) {
 // Tile shape of the fused K, V, R + WKV launch: the fewest operand lines on
 // the busiest CU (workgroups spread over 256 CUs, each reading 3 x (16*TM +
 // 16*NS) rows of C), ties to more workgroups.
-template <int S, int TM, int NS>
+template <int S, int TM, int NS, bool I8>
 int launch_kvr_wkv_shape(const KvrWkvArgs& a, hipStream_t s) {
     const int mt = (a.M + 16 * TM - 1) / (16 * TM);
     const int blocks = mt * (256 * S / (16 * NS));
-    kvr_wkv_kernel<S, TM, NS><<<blocks, 192 * S, 0, s>>>(a);
+    kvr_wkv_kernel<S, TM, NS, I8><<<blocks, 192 * S, 0, s>>>(a);
     KR_LAUNCHED();
     return KR_OK;
 }
@@ -642,23 +694,24 @@ int kvr_wkv_shape(int S, int M) {
     return bi;
 }
 
-template <int S>
+template <int S, bool I8>
 int launch_kvr_wkv_s(const KvrWkvArgs& a, hipStream_t s) {
     switch (kvr_wkv_shape(S, a.M)) {
-        case 0: return launch_kvr_wkv_shape<S, 2, 2>(a, s);
-        case 1: return launch_kvr_wkv_shape<S, 2, 1>(a, s);
-        case 2: return launch_kvr_wkv_shape<S, 1, 2>(a, s);
-        default: return launch_kvr_wkv_shape<S, 1, 1>(a, s);
+        case 0: return launch_kvr_wkv_shape<S, 2, 2, I8>(a, s);
+        case 1: return launch_kvr_wkv_shape<S, 2, 1, I8>(a, s);
+        case 2: return launch_kvr_wkv_shape<S, 1, 2, I8>(a, s);
+        default: return launch_kvr_wkv_shape<S, 1, 1, I8>(a, s);
     }
 }
 
+template <bool I8>
 int launch_kvr_wkv(int G, const KvrWkvArgs& a, hipStream_t s) {
     if (a.M == 0) return KR_OK;
     switch (G) {
-        case 1: return launch_kvr_wkv_s<1>(a, s);
-        case 2: return launch_kvr_wkv_s<2>(a, s);
-        case 3: return launch_kvr_wkv_s<3>(a, s);
-        case 4: return launch_kvr_wkv_s<4>(a, s);
+        case 1: return launch_kvr_wkv_s<1, I8>(a, s);
+        case 2: return launch_kvr_wkv_s<2, I8>(a, s);
+        case 3: return launch_kvr_wkv_s<3, I8>(a, s);
+        case 4: return launch_kvr_wkv_s<4, I8>(a, s);
         default: return kr_fail(KR_EUNSUPPORTED, "C=%d unsupported (256..1024, step 256)", 256 * G);
     }
 }
@@ -810,15 +863,33 @@ int layer_forward_q8(const kr_layer_weights& L, int C, int F, kr_half* x, int B,
     KR_TRY(launch_ln_mix<3>(G, a, s));
     set_embed(a, nullptr, x);
     KR_TRY(ph.mark(1));
-    {
-        const kr_gemm_args jobs[3] = {gemm_q8(w.kx8, w.kxs, M, C, Q.K, C, w.k, fr),
-                                      gemm_q8(w.vx8, w.vxs, M, C, Q.V, C, w.v, fr),
-                                      gemm_q8(w.rx8, w.rxs, M, C, Q.R, C, w.r, fr)};
-        const int eps[3] = {KR_EP_F32, KR_EP_F32, KR_EP_SIGMOID};
-        KR_TRY(kr_gemm_launch_multi(jobs, eps, 3, s));
-    }
-    KR_TRY(ph.mark(2));
-    {
+    if (fr && T == 1) {
+        // stepped: the three int8 products and the WKV update in one launch
+        KvrWkvArgs kw{};
+        kw.A[0] = reinterpret_cast<const kr_half*>(w.kx8);
+        kw.A[1] = reinterpret_cast<const kr_half*>(w.vx8);
+        kw.A[2] = reinterpret_cast<const kr_half*>(w.rx8);
+        kw.Wf[0] = H(Q.K.qf); kw.Wf[1] = H(Q.V.qf); kw.Wf[2] = H(Q.R.qf);
+        kw.sa[0] = w.kxs; kw.sa[1] = w.vxs; kw.sa[2] = w.rxs;
+        kw.sw[0] = Q.K.scale; kw.sw[1] = Q.V.scale; kw.sw[2] = Q.R.scale;
+        kw.decay = L.decay;
+        kw.first = L.first;
+        kw.aa = st.aa;
+        kw.bb = st.bb;
+        kw.pp = st.pp;
+        kw.ry = w.ry;
+        kw.M = M;
+        KR_TRY(launch_kvr_wkv<true>(G, kw, s));
+        KR_TRY(ph.mark(2));
+    } else {
+        {
+            const kr_gemm_args jobs[3] = {gemm_q8(w.kx8, w.kxs, M, C, Q.K, C, w.k, fr),
+                                          gemm_q8(w.vx8, w.vxs, M, C, Q.V, C, w.v, fr),
+                                          gemm_q8(w.rx8, w.rxs, M, C, Q.R, C, w.r, fr)};
+            const int eps[3] = {KR_EP_F32, KR_EP_F32, KR_EP_SIGMOID};
+            KR_TRY(kr_gemm_launch_multi(jobs, eps, 3, s));
+        }
+        KR_TRY(ph.mark(2));
         dim3 grid((C + 255) / 256, B);
         wkv_kernel<<<grid, 256, 0, s>>>(w.k, w.v, w.r, L.decay, L.first, st.aa, st.bb, st.pp,
                                         w.ry, B, T, C, 0);
@@ -916,7 +987,7 @@ int layer_step_fused(const kr_layer_weights& L, int C, int F, kr_half* x, int B,
     kw.pp = st.pp;
     kw.ry = w.ry;
     kw.M = M;
-    KR_TRY(launch_kvr_wkv(G, kw, s));
+    KR_TRY(launch_kvr_wkv<false>(G, kw, s));
     KR_TRY(ph.mark(2));
     KR_TRY(ph.mark(3));      // WKV ran inside the K/V/R launch
     KR_TRY(kr_gemm_launch(gemm_args(w.ry, M, C, L.Ot, C, x, x, nullptr, L.Of, true), KR_EP_RESID, s));
