@@ -191,7 +191,9 @@ int kr_det_matmul_packed_multi(const kr_packed_job* jobs, int n_jobs, int M, int
 
 /* w8a8 (the reference only sketches an int8 path,
  * docs/INT8_WEIGHTS_DESIGN.md): symmetric int8 with one fp32 scale per row,
- * s = max|x| / 127 (1 when the row is zero), q = clamp(rint(x / s), -127, 127).
+ * amax = max|x|, s = amax / 127, inv = 127 / amax (both 1 when the row is
+ * zero; IEEE float32 divides), q = the exact product x * inv rounded to the
+ * nearest integer, ties to even (|q| <= 127).
  * Rows are tokens for activations and output channels (rows of Wt) for
  * weights. q is [M, K] row-major, or fragment-packed (packed = 1, rows padded
  * to 16, kr_quant_bytes) for the small-M GEMM; K % 64 == 0. */
@@ -202,7 +204,11 @@ int kr_quantize_rows(const uint16_t* x, long long ldx, int M, int K, int8_t* q, 
 /* int8 GEMM: acc = sum_k xq[m,k] * wq[n,k] exactly in int32, value =
  * (float(acc) * sa[m]) * sw[n], then the epilogue of kr_det_matmul. packed = 1:
  * xq and wq fragment-packed (wq packed by kr_pack_fragments on its 16-bit
- * view, K/2 columns), M <= 512; packed = 0: both row-major [*, K]. */
+ * view, K/2 columns), M <= 512; packed = 0: both row-major [*, K];
+ * packed = 2: as 1, but xq points to fp16 activations, fragment-packed
+ * (kr_pack_fragments layout), which the product quantises per row on load
+ * by the rule above (sa is not read and may be null) - the same bits as
+ * kr_quantize_rows followed by packed = 1, in one launch. */
 int kr_det_matmul_i8(const int8_t* xq, const float* sa, int M, int K, const int8_t* wq,
                      const float* sw, int N, void* out, long long ldo, int epilogue,
                      const uint16_t* res, const uint16_t* gate, int packed, void* stream);

@@ -30,7 +30,33 @@ struct kr_gemm_args {
     int i8;
     const float* sa;    // [M] per-row (per-token) activation scales
     const float* sw;    // [N] per-output-channel weight scales
+    // w8a8, small-M fragment path only: A holds fp16 in the fp16 fragment
+    // layout (kr_frag_index) and each workgroup quantises its rows on load by
+    // the rule below, scales included (sa is not read). Same bits as
+    // quantising with kr_quantize_rows first.
+    int a_q16;
 };
+
+// w8a8 quantisation rule, one scale per row (weights: rows of W^T; activations:
+// rows = tokens):
+//   amax = max_k |x[k]|;  s = amax / 127;  inv = 127 / amax   (IEEE fp32
+//   divides; s = inv = 1 when amax = 0)
+//   q[k] = the integer nearest to the exact product x[k] * inv, ties to even
+// (|q| <= 127 since |x| <= amax). kr_q8_bits computes it with one FMA:
+// x * inv + 1.5 * 2^23 lies in [2^23, 2^24), where float32 spacing is 1, so
+// the FMA's single rounding is the integer rounding of x * inv, and the
+// result's bits are 0x4B400000 + q: their low byte is q as two's complement.
+__device__ __forceinline__ float kr_q8_inv(float amax) { return amax > 0.0f ? 127.0f / amax : 1.0f; }
+__device__ __forceinline__ float kr_q8_scale(float amax) { return amax > 0.0f ? amax / 127.0f : 1.0f; }
+__device__ __forceinline__ uint32_t kr_q8_bits(float x, float inv) {
+    return __float_as_uint(__builtin_fmaf(x, inv, 12582912.0f));
+}
+// q of x0..x3 packed into bytes 0..3 (v_perm_b32 picks the low bytes).
+__device__ __forceinline__ uint32_t kr_q8_pack4(float x0, float x1, float x2, float x3, float inv) {
+    const uint32_t lo = __builtin_amdgcn_perm(kr_q8_bits(x1, inv), kr_q8_bits(x0, inv), 0x0c0c0400u);
+    const uint32_t hi = __builtin_amdgcn_perm(kr_q8_bits(x3, inv), kr_q8_bits(x2, inv), 0x0c0c0400u);
+    return __builtin_amdgcn_perm(hi, lo, 0x05040100u);
+}
 
 // Fragment-packed layout of an [R, K] fp16 operand (K % 32 == 0, R padded to
 // a multiple of 16): the 16 x 32 block (R/16 = rb, K/32 = kb) is one

@@ -19,9 +19,12 @@
 //    added in slice order through LDS and the epilogue is shared out over the
 //    waves. Parallelism comes from the K slices, not from M.
 #include <algorithm>
+#include <climits>
 #include <type_traits>
 
 #include "kr_gemm.h"
+#include "kr_math.h"
+#include "kr_wave.h"
 #include "krunch_hip.h"
 
 namespace {
@@ -31,7 +34,8 @@ constexpr int kPitch = kBK + 8;
 constexpr int kKS = KR_GEMM_KSPLIT;
 static_assert(kKS % kBK == 0, "split must be a multiple of the LDS K tile");
 
-template <int EP>
+// DET: the w8a8 codec's sigmoid (kr_sigmoid_k); int8 kernels pass I8.
+template <int EP, bool DET = false>
 __device__ __forceinline__ void store_one(const kr_gemm_args& g, int m, int n, float acc) {
     const size_t o = (size_t)m * (size_t)g.ldo + (size_t)n;
     if constexpr (EP == KR_EP_F32) {
@@ -40,7 +44,7 @@ __device__ __forceinline__ void store_one(const kr_gemm_args& g, int m, int n, f
         const float h = (float)kr_f16(acc);
         float y;
         if constexpr (EP == KR_EP_F16) y = h;
-        else if constexpr (EP == KR_EP_SIGMOID) y = kr_sigmoid(h);
+        else if constexpr (EP == KR_EP_SIGMOID) y = kr_sigmoid_t<DET>(h);
         else if constexpr (EP == KR_EP_RELUSQ) { const float r = h > 0.0f ? h : 0.0f; y = r * r; }
         else if constexpr (EP == KR_EP_RESID) y = (float)g.res[o] + h;
         else {
@@ -207,7 +211,7 @@ __global__ void __launch_bounds__(256, 2) gemm_tile_kernel(kr_gemm_args g) {
                     float v;
                     if constexpr (I8) v = __fmul_rn(__fmul_rn((float)acc[i][j][r], g.sa[m]), g.sw[n]);
                     else v = tot[i][j][r];
-                    store_one<EP>(g, m, n, v);
+                    store_one<EP, I8>(g, m, n, v);
                 }
             }
 }
@@ -256,13 +260,13 @@ __device__ __forceinline__ void big_copy(const void* src, unsigned lds) {
 
 // Epilogue of 4 consecutive columns n..n+3 of row m (vec: aligned vector
 // access allowed and all 4 columns < N).
-template <int EP>
+template <int EP, bool DET>
 __device__ __forceinline__ void store_row4(const kr_gemm_args& g, int m, int n, kr_float4 acc,
                                            bool vec) {
     if (!vec) {
         #pragma unroll
         for (int r = 0; r < 4; r++)
-            if (n + r < g.N) store_one<EP>(g, m, n + r, acc[r]);
+            if (n + r < g.N) store_one<EP, DET>(g, m, n + r, acc[r]);
         return;
     }
     const size_t o = (size_t)m * (size_t)g.ldo + (size_t)n;
@@ -278,7 +282,7 @@ __device__ __forceinline__ void store_row4(const kr_gemm_args& g, int m, int n, 
             const float x = (float)kr_f16(acc[r]);
             float y;
             if constexpr (EP == KR_EP_F16) y = x;
-            else if constexpr (EP == KR_EP_SIGMOID) y = kr_sigmoid(x);
+            else if constexpr (EP == KR_EP_SIGMOID) y = kr_sigmoid_t<DET>(x);
             else if constexpr (EP == KR_EP_RELUSQ) { const float rr = x > 0.0f ? x : 0.0f; y = rr * rr; }
             else if constexpr (EP == KR_EP_RESID) y = (float)rv[r] + x;
             else y = (float)rv[r] + (float)kr_f16((float)gv[r] * x);
@@ -447,7 +451,7 @@ __global__ void __launch_bounds__(512, 1) gemm_big_kernel(kr_gemm_args g, int n_
             #pragma unroll
             for (int t = 0; t < 4; t++) {
                 const int n = n0 + 64 * wn + 16 * t + 4 * lq;
-                store_row4<EP>(g, m, n, tot[i][t], vec_ok && n + 3 < g.N);
+                store_row4<EP, I8>(g, m, n, tot[i][t], vec_ok && n + 3 < g.N);
             }
         }
         if (!has_next) break;
@@ -507,10 +511,20 @@ int launch_big(const kr_gemm_args& g, int ep, hipStream_t s) {
 // workgroups of one column group (which share its weight panels) all land on
 // the same XCD (workgroups are dealt to the 8 XCDs round robin), so each
 // weight byte is fetched into one L2.
+//
+// QA (w8a8, a_q16): A arrives as fp16 in the fp16 fragment layout and is
+// quantised here, one scale per row: each wave takes max |x| over its slice
+// of its rows, the waves meet in LDS for the row maximum, and every wave
+// rounds its own slice to int8 (kr_q8_pack4) in registers. The bits are those
+// of kr_quantize_rows followed by the int8 product, without the separate
+// quantisation launch; the cost is twice the A bytes.
 constexpr int kEpiPrefetch = 4;   // epilogue tiles per wave with prefetched res/gate
 
-template <int TM, int NS, bool FRAG, int MAXT, bool I8>
+typedef unsigned short kr_u16x2 __attribute__((ext_vector_type(2)));
+
+template <int TM, int NS, bool FRAG, int MAXT, bool I8, bool QA>
 __global__ void __launch_bounds__(MAXT) gemm_panel_kernel(kr_gemm_multi mj) {
+    static_assert(!QA || (I8 && FRAG), "on-load quantisation needs the int8 fragment path");
     constexpr int TT = TM * NS;
     // 1 KB operand blocks per wave slice: 8 x (16x32 fp16) or 4 x (16x64 int8);
     // either way a wave covers 256 k. int8 operands move as 16-bit pairs.
@@ -547,6 +561,10 @@ __global__ void __launch_bounds__(MAXT) gemm_panel_kernel(kr_gemm_multi mj) {
     // ---- operand loads: A once, W panels double buffered
     kr_half8 a[TM][QPS];
     kr_half8 b[2][QPS];
+    // QA: int8 block q of the slice holds, in lane (r, j) = (l % 16, l / 16),
+    // the 16 halves k = 64q + 16j .. +15 of row r: fp16 block 2q + j/2 of the
+    // slice, lanes r + 32(j % 2) and r + 32(j % 2) + 16.
+    kr_half8 af[QA ? TM : 1][QA ? QPS : 1][2];
     const int kb = (I8 ? g.K >> 1 : g.K) >> 5;   // 1 KB blocks per row
     auto load_w = [&](int t, kr_half8 (&dst)[QPS]) {
         // panels beyond N re-read the last one; their outputs are never stored
@@ -564,7 +582,16 @@ __global__ void __launch_bounds__(MAXT) gemm_panel_kernel(kr_gemm_multi mj) {
     };
     #pragma unroll
     for (int i = 0; i < TM; i++) {
-        if constexpr (FRAG) {
+        if constexpr (QA) {
+            const int mb = min((m0 >> 4) + i, last_mb), j16 = lane >> 4;
+            const kr_half* ap = g.A + ((size_t)mb * (g.K >> 5) + 8 * s + (j16 >> 1)) * 512 +
+                                ((lane & 15) + 32 * (j16 & 1)) * 8;
+            #pragma unroll
+            for (int q = 0; q < QPS; q++) {
+                af[i][q][0] = *reinterpret_cast<const kr_half8*>(ap + 1024 * q);
+                af[i][q][1] = *reinterpret_cast<const kr_half8*>(ap + 1024 * q + 128);
+            }
+        } else if constexpr (FRAG) {
             const int mb = min((m0 >> 4) + i, last_mb);
             const kr_half* ap = g.A + ((size_t)mb * kb + QPS * s) * 512 + lane * 8;
             #pragma unroll
@@ -610,6 +637,59 @@ __global__ void __launch_bounds__(MAXT) gemm_panel_kernel(kr_gemm_multi mj) {
     }
     __builtin_amdgcn_sched_barrier(0);     // loads in flight before the MFMAs
 
+    // ---- QA: row maxima over all slices, then this slice rounded to int8
+    float amax_r[TM];                      // QA: row maximum, then row scale
+    if constexpr (QA) {
+        float* qmax = part_lds + (size_t)S * TT * 256;     // [S][TM][16]
+        #pragma unroll
+        for (int i = 0; i < TM; i++) {
+            // |x| as fp16 bit patterns: unsigned order is value order (finite x)
+            kr_u16x2 m2 = {0, 0};
+            #pragma unroll
+            for (int q = 0; q < QPS; q++)
+                #pragma unroll
+                for (int h = 0; h < 2; h++) {
+                    const kr_int4 w4 = __builtin_bit_cast(kr_int4, af[i][q][h]);
+                    #pragma unroll
+                    for (int d = 0; d < 4; d++)
+                        m2 = __builtin_elementwise_max(
+                            m2, __builtin_bit_cast(kr_u16x2, (unsigned)w4[d] & 0x7fff7fffu));
+                }
+            unsigned mm = m2[0] > m2[1] ? m2[0] : m2[1];
+            mm = max(mm, kr_xor<16>(mm));
+            mm = max(mm, kr_xor<32>(mm));
+            amax_r[i] = (float)__builtin_bit_cast(kr_half, (unsigned short)mm);
+            if (S > 1 && lane < 16) qmax[(s * TM + i) * 16 + lane] = amax_r[i];
+        }
+        if (S > 1) {
+            __syncthreads();
+            #pragma unroll
+            for (int i = 0; i < TM; i++) {
+                float am = qmax[i * 16 + (lane & 15)];
+                for (int q = 1; q < S; q++) am = fmaxf(am, qmax[(q * TM + i) * 16 + (lane & 15)]);
+                amax_r[i] = am;
+            }
+        }
+        #pragma unroll
+        for (int i = 0; i < TM; i++) {
+            const float inv = kr_q8_inv(amax_r[i]);
+            const float sc = kr_q8_scale(amax_r[i]);
+            #pragma unroll
+            for (int q = 0; q < QPS; q++) {
+                kr_int4 w4;
+                #pragma unroll
+                for (int d = 0; d < 4; d++) {
+                    const kr_half8& h = af[i][q][d >> 1];
+                    const int e = 4 * (d & 1);
+                    w4[d] = (int)kr_q8_pack4((float)h[e], (float)h[e + 1], (float)h[e + 2],
+                                             (float)h[e + 3], inv);
+                }
+                a[i][q] = __builtin_bit_cast(kr_half8, w4);
+            }
+            amax_r[i] = sc;                // from here on: the row's scale
+        }
+    }
+
     // ---- MFMA chains, one per (row block, panel)
     Acc p[TM][NS];
     #pragma unroll
@@ -633,7 +713,16 @@ __global__ void __launch_bounds__(MAXT) gemm_panel_kernel(kr_gemm_multi mj) {
     auto dequant = [&](int t, kr_int4 acc) -> kr_float4 {
         int m, nb;
         tile_mn(t, m, nb);
-        const float sa = g.sa[min(m, g.M - 1)];
+        float sa;
+        if constexpr (QA) {
+            // the lane's row of row block t / NS is the one amax_r holds
+            sa = amax_r[0];
+            #pragma unroll
+            for (int i = 1; i < TM; i++)
+                if (t / NS == i) sa = amax_r[i];
+        } else {
+            sa = g.sa[min(m, g.M - 1)];
+        }
         kr_float4 y;
         #pragma unroll
         for (int r = 0; r < 4; r++) y[r] = __fmul_rn(__fmul_rn((float)acc[r], sa), g.sw[min(nb + r, g.N - 1)]);
@@ -668,7 +757,7 @@ __global__ void __launch_bounds__(MAXT) gemm_panel_kernel(kr_gemm_multi mj) {
                 const float x = (float)kr_f16(acc[r]);
                 float y;
                 if (ep == KR_EP_F16) y = x;
-                else if (ep == KR_EP_SIGMOID) y = kr_sigmoid(x);
+                else if (ep == KR_EP_SIGMOID) y = kr_sigmoid_t<I8>(x);
                 else if (ep == KR_EP_RELUSQ) { const float rr = x > 0.0f ? x : 0.0f; y = rr * rr; }
                 else if (ep == KR_EP_RESID) y = (float)rv[r] + x;
                 else y = (float)rv[r] + (float)kr_f16((float)gv[r] * x);
@@ -682,12 +771,12 @@ __global__ void __launch_bounds__(MAXT) gemm_panel_kernel(kr_gemm_multi mj) {
             for (int r = 0; r < 4; r++)
                 if (nb + r < g.N) {
                     switch (ep) {
-                        case KR_EP_F32: store_one<KR_EP_F32>(g, m, nb + r, acc[r]); break;
-                        case KR_EP_F16: store_one<KR_EP_F16>(g, m, nb + r, acc[r]); break;
-                        case KR_EP_SIGMOID: store_one<KR_EP_SIGMOID>(g, m, nb + r, acc[r]); break;
-                        case KR_EP_RELUSQ: store_one<KR_EP_RELUSQ>(g, m, nb + r, acc[r]); break;
-                        case KR_EP_RESID: store_one<KR_EP_RESID>(g, m, nb + r, acc[r]); break;
-                        default: store_one<KR_EP_GATED>(g, m, nb + r, acc[r]); break;
+                        case KR_EP_F32: store_one<KR_EP_F32, I8>(g, m, nb + r, acc[r]); break;
+                        case KR_EP_F16: store_one<KR_EP_F16, I8>(g, m, nb + r, acc[r]); break;
+                        case KR_EP_SIGMOID: store_one<KR_EP_SIGMOID, I8>(g, m, nb + r, acc[r]); break;
+                        case KR_EP_RELUSQ: store_one<KR_EP_RELUSQ, I8>(g, m, nb + r, acc[r]); break;
+                        case KR_EP_RESID: store_one<KR_EP_RESID, I8>(g, m, nb + r, acc[r]); break;
+                        default: store_one<KR_EP_GATED, I8>(g, m, nb + r, acc[r]); break;
                     }
                 }
         }
@@ -735,7 +824,7 @@ struct PanelShape {
     int TM, NS;
 };
 
-template <int TM, int NS, bool FRAG, int MAXT, bool I8>
+template <int TM, int NS, bool FRAG, int MAXT, bool I8, bool QA>
 int launch_panel(kr_gemm_multi mj, hipStream_t s) {
     const int S = mj.job[0].K / kKS;
     int total = 0;
@@ -744,8 +833,9 @@ int launch_panel(kr_gemm_multi mj, hipStream_t s) {
         mj.tiles[j] = ((g.M + 16 * TM - 1) / (16 * TM)) * ((g.N + 16 * NS - 1) / (16 * NS));
         total += mj.tiles[j];
     }
-    const size_t lds = S > 1 ? (size_t)S * TM * NS * 256 * sizeof(float) : 0;
-    gemm_panel_kernel<TM, NS, FRAG, MAXT, I8><<<total, dim3(64 * S), lds, s>>>(mj);
+    size_t lds = S > 1 ? (size_t)S * TM * NS * 256 * sizeof(float) : 0;
+    if (QA && S > 1) lds += (size_t)S * TM * 16 * sizeof(float);
+    gemm_panel_kernel<TM, NS, FRAG, MAXT, I8, QA><<<total, dim3(64 * S), lds, s>>>(mj);
     KR_LAUNCHED();
     return KR_OK;
 }
@@ -762,8 +852,9 @@ constexpr PanelShape kShapes768[] = {{1, 1}, {1, 2}, {2, 1}, {2, 2}};
 constexpr PanelShape kShapes1024[] = {{1, 1}, {1, 2}};
 
 // Busiest-CU operand bytes (in 128-byte lines) for a shape: workgroups are
-// spread over the 256 CUs, each reading (16*TM + 16*NS) x K halves; ties go
-// to the shape that occupies more CUs.
+// spread over the 256 CUs, each reading (16*TM + 16*NS) x K halves (QA: A
+// rows count twice against int8 weight rows); ties go to the shape that
+// occupies more CUs.
 long long panel_cost(const kr_gemm_multi& mj, PanelShape sh) {
     long long wgs = 0;
     for (int j = 0; j < mj.njobs; j++) {
@@ -771,7 +862,10 @@ long long panel_cost(const kr_gemm_multi& mj, PanelShape sh) {
         wgs += (long long)((g.M + 16 * sh.TM - 1) / (16 * sh.TM)) *
                ((g.N + 16 * sh.NS - 1) / (16 * sh.NS));
     }
-    const long long per_wg = (long long)(sh.TM + sh.NS) * mj.job[0].K / 4;
+    // QA with 4 row blocks needs more registers than a wave has (spills)
+    if (mj.job[0].a_q16 && sh.TM > 2) return LLONG_MAX;
+    const int ta = mj.job[0].a_q16 ? 2 * sh.TM : sh.TM;
+    const long long per_wg = (long long)(ta + sh.NS) * mj.job[0].K / 4;
     return ((wgs + 255) / 256) * per_wg * 4096 - std::min<long long>(wgs, 256);
 }
 
@@ -793,13 +887,14 @@ PanelShape choose_small_shape(const kr_gemm_multi& mj) {
     return choose_shape(mj, kShapes1024);
 }
 
-template <bool FRAG, int MAXT, bool I8, size_t N>
+template <bool FRAG, int MAXT, bool I8, bool QA, size_t N>
 int launch_best(const kr_gemm_multi& mj, const PanelShape (&shapes)[N], hipStream_t s) {
     const PanelShape best = choose_shape(mj, shapes);
 #define KR_PANEL(TM_, NS_) \
-    if (best.TM == TM_ && best.NS == NS_) return launch_panel<TM_, NS_, FRAG, MAXT, I8>(mj, s);
+    if (best.TM == TM_ && best.NS == NS_) return launch_panel<TM_, NS_, FRAG, MAXT, I8, QA>(mj, s);
     if constexpr (MAXT == 256) {
-        KR_PANEL(1, 1) KR_PANEL(1, 2) KR_PANEL(2, 1) KR_PANEL(2, 2) KR_PANEL(4, 1) KR_PANEL(4, 2)
+        KR_PANEL(1, 1) KR_PANEL(1, 2) KR_PANEL(2, 1) KR_PANEL(2, 2)
+        if constexpr (!QA) { KR_PANEL(4, 1) KR_PANEL(4, 2) }
     } else if constexpr (MAXT == 768) {
         KR_PANEL(1, 1) KR_PANEL(1, 2) KR_PANEL(2, 1) KR_PANEL(2, 2)
     } else {
@@ -809,12 +904,12 @@ int launch_best(const kr_gemm_multi& mj, const PanelShape (&shapes)[N], hipStrea
     return kr_fail(KR_EINVAL, "gemm: no panel shape");
 }
 
-template <bool FRAG, bool I8>
+template <bool FRAG, bool I8, bool QA = false>
 int launch_small(const kr_gemm_multi& mj, hipStream_t s) {
     const int S = mj.job[0].K / kKS;
-    if (S <= 4) return launch_best<FRAG, 256, I8>(mj, kShapes256, s);
-    if (S <= 12) return launch_best<FRAG, 768, I8>(mj, kShapes768, s);
-    return launch_best<FRAG, 1024, I8>(mj, kShapes1024, s);
+    if (S <= 4) return launch_best<FRAG, 256, I8, QA>(mj, kShapes256, s);
+    if (S <= 12) return launch_best<FRAG, 768, I8, QA>(mj, kShapes768, s);
+    return launch_best<FRAG, 1024, I8, QA>(mj, kShapes1024, s);
 }
 
 // ---------------------------------------------------------------------------
@@ -1016,7 +1111,7 @@ int check_args(const kr_gemm_args& g, int ep) {
                                ep != KR_EP_GATED && ((uintptr_t)g.out & 7) == 0),
                "gemm: fragment-packed output needs N %% 32 == 0 and an elementwise fp16 epilogue");
     KR_REQUIRE(ep >= KR_EP_F32 && ep <= KR_EP_GATED, "gemm: unknown epilogue %d", ep);
-    KR_REQUIRE(!g.i8 || (g.sa && g.sw && (g.a_frag || g.lda % 16 == 0) &&
+    KR_REQUIRE(!g.i8 || ((g.sa || g.a_q16) && g.sw && (g.a_frag || g.lda % 16 == 0) &&
                          (!g.Wt || g.ldw % 16 == 0)),
                "gemm: int8 needs scales and 16-byte aligned rows (lda/ldw multiples of 16)");
     KR_REQUIRE((ep != KR_EP_RESID && ep != KR_EP_GATED) || g.res, "gemm: residual missing");
@@ -1040,10 +1135,13 @@ int kr_gemm_launch_multi(const kr_gemm_args* jobs, const int* eps, int njobs, hi
     }
     const int M = jobs[0].M, K = jobs[0].K;
     bool same = true, small_n = true, frag = jobs[0].a_frag != 0, any_frag = false;
-    const bool i8 = jobs[0].i8 != 0;
+    const bool i8 = jobs[0].i8 != 0, qa = jobs[0].a_q16 != 0;
     for (int j = 1; j < njobs; j++)
         same = same && jobs[j].M == M && jobs[j].K == K && (jobs[j].a_frag != 0) == frag &&
-               (jobs[j].i8 != 0) == i8;
+               (jobs[j].i8 != 0) == i8 && (jobs[j].a_q16 != 0) == qa;
+    for (int j = 0; j < njobs; j++)
+        KR_REQUIRE(!jobs[j].a_q16 || (jobs[j].i8 && jobs[j].a_frag && jobs[j].Wf),
+                   "gemm: on-load quantisation needs int8 weights and fragment-packed operands");
     for (int j = 0; j < njobs; j++) {
         small_n = small_n && jobs[j].N < KR_GEMM_SMALL_MAX_N;
         any_frag = any_frag || jobs[j].a_frag || jobs[j].out_frag;
@@ -1057,6 +1155,7 @@ int kr_gemm_launch_multi(const kr_gemm_args* jobs, const int* eps, int njobs, hi
         kr_gemm_multi mj{};
         mj.njobs = njobs;
         for (int j = 0; j < njobs; j++) { mj.job[j] = jobs[j]; mj.ep[j] = eps[j]; }
+        if (qa) return launch_small<true, true, true>(mj, s);
         if (frag) return i8 ? launch_small<true, true>(mj, s) : launch_small<true, false>(mj, s);
         // row-major A: fragment weights are not used, the row-major copy must exist
         for (int j = 0; j < njobs; j++) KR_REQUIRE(jobs[j].Wt, "gemm: row-major W missing");

@@ -19,6 +19,7 @@
 #include <vector>
 
 #include "kr_gemm.h"
+#include "kr_math.h"
 #include "kr_model.h"
 #include "kr_wave.h"
 
@@ -152,9 +153,8 @@ __device__ __forceinline__ void store_mix(kr_half* __restrict__ out, size_t row,
     }
 }
 
-// w8a8: the fp16 mix row quantised per row (symmetric int8, s = max|v| / 127,
-// q = clamp(rint(v / s), -127, 127); the rule of kr_quantize_rows), row-major
-// or fragment-packed for the small-M int8 GEMM.
+// w8a8: the fp16 mix row quantised per row by the rule of kr_quantize_rows
+// (kr_gemm.h), row-major or fragment-packed for the small-M int8 GEMM.
 template <int G>
 __device__ __forceinline__ void store_mix_q8(int8_t* __restrict__ out, float* __restrict__ scales,
                                              size_t row, bool frag, const CoefH<G>& tm, int lane,
@@ -171,20 +171,15 @@ __device__ __forceinline__ void store_mix_q8(int8_t* __restrict__ out, float* __
             amax = fmaxf(amax, fabsf(v[i][q]));
         }
     amax = kr_wave_reduce(amax, [](float a, float b) { return fmaxf(a, b); });
-    const float s = amax > 0.0f ? amax / 127.0f : 1.0f;
+    const float inv = kr_q8_inv(amax);
     #pragma unroll
     for (int i = 0; i < G; i++) {
-        uint32_t w = 0;
-        #pragma unroll
-        for (int q = 0; q < 4; q++) {
-            const float r = fminf(fmaxf(rintf(v[i][q] / s), -127.0f), 127.0f);
-            w |= ((uint32_t)(uint8_t)(int8_t)(int)r) << (8 * q);
-        }
+        const uint32_t w = kr_q8_pack4(v[i][0], v[i][1], v[i][2], v[i][3], inv);
         const int col = 256 * i + 4 * lane;
         const size_t o = frag ? kr_frag_index_i8((long long)row, col, C) : row * C + col;
         *reinterpret_cast<uint32_t*>(out + o) = w;
     }
-    if (lane == 0) scales[row] = s;
+    if (lane == 0) scales[row] = kr_q8_scale(amax);
 }
 
 // Weight panels to pull into each XCD's L2 while a latency-bound LN-mix runs:
@@ -346,22 +341,25 @@ struct WkvState {
 };
 
 // One token of the recurrence; returns ry.
+// DET: exps by kr_kexp (the w8a8 codec; every argument here is <= 0).
+template <bool DET>
 __device__ __forceinline__ kr_half wkv_token(WkvState& st, float w, float u, float kk, float vv,
                                              float rr) {
     const float ww = u + kk;
     const float p1 = fmaxf(st.p, ww);
-    const float e1 = __expf(st.p - p1), e2 = __expf(ww - p1);
+    const float e1 = kr_exp_t<DET>(st.p - p1), e2 = kr_exp_t<DET>(ww - p1);
     const float y = (e1 * st.a + e2 * vv) / (e1 * st.b + e2);
     const kr_half ry = kr_f16(rr * (float)kr_f16(y));
     const float ww2 = w + st.p;
     const float p2 = fmaxf(ww2, kk);
-    const float f1 = __expf(ww2 - p2), f2 = __expf(kk - p2);
+    const float f1 = kr_exp_t<DET>(ww2 - p2), f2 = kr_exp_t<DET>(kk - p2);
     st.a = f1 * st.a + f2 * vv;
     st.b = f1 * st.b + f2;
     st.p = p2;
     return ry;
 }
 
+template <bool DET>
 __global__ void __launch_bounds__(256) wkv_kernel(const float* __restrict__ k,
                                                   const float* __restrict__ v,
                                                   const kr_half* __restrict__ r,
@@ -382,7 +380,7 @@ __global__ void __launch_bounds__(256) wkv_kernel(const float* __restrict__ k,
     auto ry_at = [&](int t) -> size_t {
         return ry_frag ? kr_frag_index((long long)b * T + t, c, C) : base + (size_t)t * C;
     };
-    ry[ry_at(0)] = wkv_token(st, w, u, k0, v0, r0);
+    ry[ry_at(0)] = wkv_token<DET>(st, w, u, k0, v0, r0);
     for (int t0 = 1; t0 < T; t0 += kWkvChunk) {
         float kk[kWkvChunk], vv[kWkvChunk], rr[kWkvChunk];
         #pragma unroll
@@ -396,7 +394,7 @@ __global__ void __launch_bounds__(256) wkv_kernel(const float* __restrict__ k,
         }
         #pragma unroll
         for (int q = 0; q < kWkvChunk; q++)
-            if (t0 + q < T) ry[ry_at(t0 + q)] = wkv_token(st, w, u, kk[q], vv[q], rr[q]);
+            if (t0 + q < T) ry[ry_at(t0 + q)] = wkv_token<DET>(st, w, u, kk[q], vv[q], rr[q]);
     }
     aa[s] = st.a;
     bb[s] = st.b;
@@ -429,8 +427,8 @@ struct KvrWkvArgs {
     float* aa;                 // [M, C] WKV state, updated in place
     float* bb;
     float* pp;
-    kr_half* ry;               // fragment-packed [M16, C] (K = C operand of the output GEMM)
-                               // or, for w8a8, row-major [M, C] (the quantiser's input)
+    kr_half* ry;               // fragment-packed [M16, C] (K = C operand of the output GEMM;
+                               // for w8a8 quantised by that product on load)
     int M;
 };
 
@@ -447,7 +445,7 @@ __device__ __forceinline__ void lds_dma16(const void* src, void* lds_base) {
 // I8 (w8a8): int8 operands in the same 1 KB block layout (a 16 x 64 int8
 // block is the 16 x 32 block of the 16-bit view), v_mfma_i32_16x16x64_i8,
 // the slice partials summed exactly in int32, then value = (float(acc) *
-// sa[m]) * sw[n], the int8 GEMM's dequantisation; ry is written row-major.
+// sa[m]) * sw[n], the int8 GEMM's dequantisation.
 template <int S, int TM, int NS, bool I8>
 __global__ void __launch_bounds__(192 * S) kvr_wkv_kernel(KvrWkvArgs a) {
     constexpr int C = 256 * S, NW = 3 * S, TT = TM * NS;
@@ -583,9 +581,9 @@ __global__ void __launch_bounds__(192 * S) kvr_wkv_kernel(KvrWkvArgs a) {
         kr_half4 ry;
         #pragma unroll
         for (int e = 0; e < 4; e++) {
-            const float r = (float)kr_f16(kr_sigmoid((float)kr_f16(rv[e])));
+            const float r = (float)kr_f16(kr_sigmoid_t<I8>((float)kr_f16(rv[e])));
             WkvState st{sa[e], sb[e], sp[e]};
-            ry[e] = wkv_token(st, dw[e], du[e], k[e], v[e], r);
+            ry[e] = wkv_token<I8>(st, dw[e], du[e], k[e], v[e], r);
             sa[e] = st.a;
             sb[e] = st.b;
             sp[e] = st.p;
@@ -594,8 +592,7 @@ __global__ void __launch_bounds__(192 * S) kvr_wkv_kernel(KvrWkvArgs a) {
         *reinterpret_cast<kr_float4*>(a.aa + o) = sa;
         *reinterpret_cast<kr_float4*>(a.bb + o) = sb;
         *reinterpret_cast<kr_float4*>(a.pp + o) = sp;
-        if constexpr (I8) *reinterpret_cast<kr_half4*>(a.ry + o) = ry;
-        else *reinterpret_cast<kr_half4*>(a.ry + kr_frag_index(em, en, C)) = ry;
+        *reinterpret_cast<kr_half4*>(a.ry + kr_frag_index(em, en, C)) = ry;
     }
 }
 
@@ -811,8 +808,11 @@ struct Phases {
 };
 
 // w8a8 layer: the same op order with the seven products on
-// int8 MFMA. LN-mix writes its operands quantised per row; the WKV output and
-// the ReLU^2 output are quantised by a row kernel before their products.
+// int8 MFMA. LN-mix writes its operands quantised per row. On the small-M
+// fragment path the output projection and the channel-mix value product
+// quantise their fp16 operands (the WKV output, the ReLU^2 output) on load;
+// on the large-M path a row kernel quantises them first. Both give the same
+// int8 operands and scales.
 kr_gemm_args gemm_q8(const int8_t* A, const float* sa, int M, int K, const kr_matrix_q8& W,
                      int N, void* out, bool fr, const kr_half* res = nullptr,
                      const kr_half* gate = nullptr) {
@@ -821,6 +821,16 @@ kr_gemm_args gemm_q8(const int8_t* A, const float* sa, int M, int K, const kr_ma
     g.i8 = 1;
     g.sa = sa;
     g.sw = W.scale;
+    return g;
+}
+
+// The same with A as fp16 fragment-packed, quantised per row by the product.
+kr_gemm_args gemm_q8_q16(const kr_half* A, int M, int K, const kr_matrix_q8& W, int N, void* out,
+                         const kr_half* res = nullptr, const kr_half* gate = nullptr) {
+    kr_gemm_args g = gemm_args(A, M, K, W.q, N, out, res, gate, W.qf, true);
+    g.i8 = 1;
+    g.sw = W.scale;
+    g.a_q16 = 1;
     return g;
 }
 
@@ -891,13 +901,17 @@ int layer_forward_q8(const kr_layer_weights& L, int C, int F, kr_half* x, int B,
         }
         KR_TRY(ph.mark(2));
         dim3 grid((C + 255) / 256, B);
-        wkv_kernel<<<grid, 256, 0, s>>>(w.k, w.v, w.r, L.decay, L.first, st.aa, st.bb, st.pp,
-                                        w.ry, B, T, C, 0);
+        wkv_kernel<true><<<grid, 256, 0, s>>>(w.k, w.v, w.r, L.decay, L.first, st.aa, st.bb, st.pp,
+                                        w.ry, B, T, C, fr ? 1 : 0);
         KR_LAUNCHED();
     }
-    KR_TRY(kr_impl_quantize_rows(w.ry, C, M, C, w.ry8, w.rys, fr ? 1 : 0, s));
     KR_TRY(ph.mark(3));
-    KR_TRY(kr_gemm_launch(gemm_q8(w.ry8, w.rys, M, C, Q.O, C, x, fr, x), KR_EP_RESID, s));
+    if (fr) {
+        KR_TRY(kr_gemm_launch(gemm_q8_q16(w.ry, M, C, Q.O, C, x, x), KR_EP_RESID, s));
+    } else {
+        KR_TRY(kr_impl_quantize_rows(w.ry, C, M, C, w.ry8, w.rys, 0, s));
+        KR_TRY(kr_gemm_launch(gemm_q8(w.ry8, w.rys, M, C, Q.O, C, x, false, x), KR_EP_RESID, s));
+    }
     KR_TRY(ph.mark(4));
     a.ln_w = H(L.ln2_w);
     a.ln_b = H(L.ln2_b);
@@ -908,14 +922,20 @@ int layer_forward_q8(const kr_layer_weights& L, int C, int F, kr_half* x, int B,
     KR_TRY(launch_ln_mix<2>(G, a, s));
     KR_TRY(ph.mark(5));
     {
-        const kr_gemm_args jobs[2] = {gemm_q8(w.frx8, w.frxs, M, C, Q.fR, C, w.rf, fr),
-                                      gemm_q8(w.fkx8, w.fkxs, M, C, Q.fK, F, w.kf, fr)};
+        kr_gemm_args jobs[2] = {gemm_q8(w.frx8, w.frxs, M, C, Q.fR, C, w.rf, fr),
+                                gemm_q8(w.fkx8, w.fkxs, M, C, Q.fK, F, w.kf, fr)};
+        jobs[1].out_frag = fr ? 1 : 0;     // the value product's fp16 operand
         const int eps[2] = {KR_EP_SIGMOID, KR_EP_RELUSQ};
         KR_TRY(kr_gemm_launch_multi(jobs, eps, 2, s));
     }
-    KR_TRY(kr_impl_quantize_rows(w.kf, F, M, F, w.kf8, w.kfs, fr ? 1 : 0, s));
     KR_TRY(ph.mark(6));
-    KR_TRY(kr_gemm_launch(gemm_q8(w.kf8, w.kfs, M, F, Q.fV, C, x, fr, x, w.rf), KR_EP_GATED, s));
+    if (fr) {
+        KR_TRY(kr_gemm_launch(gemm_q8_q16(w.kf, M, F, Q.fV, C, x, x, w.rf), KR_EP_GATED, s));
+    } else {
+        KR_TRY(kr_impl_quantize_rows(w.kf, F, M, F, w.kf8, w.kfs, 0, s));
+        KR_TRY(kr_gemm_launch(gemm_q8(w.kf8, w.kfs, M, F, Q.fV, C, x, false, x, w.rf),
+                              KR_EP_GATED, s));
+    }
     return ph.mark(7);
 }
 
@@ -1046,7 +1066,7 @@ int layer_forward(const kr_layer_weights& L, int C, int F, kr_half* x, int B, in
     KR_TRY(ph.mark(2));
     {
         dim3 grid((C + 255) / 256, B);
-        wkv_kernel<<<grid, 256, 0, s>>>(w.k, w.v, w.r, L.decay, L.first, st.aa, st.bb, st.pp,
+        wkv_kernel<false><<<grid, 256, 0, s>>>(w.k, w.v, w.r, L.decay, L.first, st.aa, st.bb, st.pp,
                                         w.ry, B, T, C, fr ? 1 : 0);
         KR_LAUNCHED();
     }
@@ -1392,7 +1412,7 @@ int kr_wkv(int B, int T, int C, const float* decay, const float* first, const fl
     KR_REQUIRE(B >= 1 && T >= 0 && C >= 1, "kr_wkv: bad shape");
     if (T == 0) return KR_OK;
     dim3 grid((C + 255) / 256, B);
-    wkv_kernel<<<grid, 256, 0, kr_stream(stream)>>>(k, v, reinterpret_cast<const kr_half*>(r),
+    wkv_kernel<false><<<grid, 256, 0, kr_stream(stream)>>>(k, v, reinterpret_cast<const kr_half*>(r),
                                                     decay, first, aa, bb, pp,
                                                     reinterpret_cast<kr_half*>(ry), B, T, C, 0);
     KR_LAUNCHED();

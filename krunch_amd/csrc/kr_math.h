@@ -1,4 +1,5 @@
-// Deterministic float32 exp used by the head softmax.
+// Deterministic float32 exp used by the head softmax and, in the w8a8 codec,
+// by the sigmoid and the WKV update.
 //
 // Cody-Waite reduction x = n*ln2 + r (ln2 split into a 15-bit high part and a
 // low part, each step a fused multiply-add), degree-7 Taylor polynomial of
@@ -36,4 +37,27 @@ __device__ __forceinline__ float kr_kexp(float x) {
     p = __builtin_fmaf(p, r, 1.0f);
     const float y = __builtin_ldexpf(p, (int)n);
     return x >= -87.0f ? y : 0.0f;
+}
+
+// Logistic function from kr_kexp (its argument -|x| is never positive):
+// 1 / (1 + e) for x >= 0, e / (1 + e) for x < 0, e = exp(-|x|). Used by the
+// w8a8 codec, whose every activation feeds a rounding to int8: with a
+// restatable exp the CPU oracle reproduces its activations bit for bit.
+__device__ __forceinline__ float kr_sigmoid_k(float x) {
+    const float e = kr_kexp(-fabsf(x));
+    const float d = 1.0f + e;
+    return x >= 0.0f ? 1.0f / d : e / d;
+}
+
+// DET selects kr_kexp / kr_sigmoid_k (the w8a8 codec) over the hardware
+// exp (the fp16 codec).
+template <bool DET>
+__device__ __forceinline__ float kr_exp_t(float x) {
+    if constexpr (DET) return kr_kexp(x);
+    else return __expf(x);
+}
+template <bool DET>
+__device__ __forceinline__ float kr_sigmoid_t(float x) {
+    if constexpr (DET) return kr_sigmoid_k(x);
+    else return kr_sigmoid(x);
 }

@@ -2,8 +2,10 @@
 // one scale per row. Used for the weights (rows of W^T = output channels) at
 // preparation time and for activations (rows = tokens) on the fly.
 //
-//   amax = max_k |x[k]|;  s = amax / 127 (s = 1 when amax = 0)
-//   q[k] = clamp(rint(x[k] / s), -127, 127)          (IEEE divide, ties to even)
+//   amax = max_k |x[k]|;  s = amax / 127;  inv = 127 / amax   (s = inv = 1
+//   when amax = 0; IEEE divides)
+//   q[k] = round(x[k] * inv), the exact product rounded to the nearest
+//          integer, ties to even (kr_q8_bits in kr_gemm.h: one FMA)
 //
 // so the int8 GEMM value (float(sum q_a q_w) * s_a) * s_w approximates x @ W.
 // The output is row-major [M, K] int8 or fragment-packed (kr_frag_index_i8),
@@ -18,16 +20,6 @@ __device__ __forceinline__ float wave_maxf(float v) {
     return v;
 }
 
-__device__ __forceinline__ uint32_t pack4(const float (&x)[4], float s) {
-    uint32_t w = 0;
-    #pragma unroll
-    for (int r = 0; r < 4; r++) {
-        float q = rintf(x[r] / s);
-        q = fminf(fmaxf(q, -127.0f), 127.0f);
-        w |= ((uint32_t)(uint8_t)(int8_t)(int)q) << (8 * r);
-    }
-    return w;
-}
 
 // One wave per row; lane l owns the 4-column groups at 256*i + 4*l.
 __global__ void __launch_bounds__(256) row_quant_kernel(const kr_half* __restrict__ x, long long ldx,
@@ -44,14 +36,14 @@ __global__ void __launch_bounds__(256) row_quant_kernel(const kr_half* __restric
         for (int r = 0; r < 4; r++) amax = fmaxf(amax, fabsf((float)h[r]));
     }
     amax = wave_maxf(amax);
-    const float s = amax > 0.0f ? amax / 127.0f : 1.0f;
+    const float inv = kr_q8_inv(amax);
     for (int c = 4 * lane; c < K; c += 256) {
         const kr_half4 h = *reinterpret_cast<const kr_half4*>(xr + c);
-        const float v[4] = {(float)h[0], (float)h[1], (float)h[2], (float)h[3]};
         const size_t o = packed ? kr_frag_index_i8(row, c, K) : (size_t)row * (size_t)K + c;
-        *reinterpret_cast<uint32_t*>(q + o) = pack4(v, s);
+        *reinterpret_cast<uint32_t*>(q + o) =
+            kr_q8_pack4((float)h[0], (float)h[1], (float)h[2], (float)h[3], inv);
     }
-    if (lane == 0) scales[row] = s;
+    if (lane == 0) scales[row] = kr_q8_scale(amax);
 }
 
 }  // namespace
@@ -83,6 +75,7 @@ int kr_quantize_rows(const uint16_t* x, long long ldx, int M, int K, int8_t* q, 
 int kr_det_matmul_i8(const int8_t* xq, const float* sa, int M, int K, const int8_t* wq,
                      const float* sw, int N, void* out, long long ldo, int epilogue,
                      const uint16_t* res, const uint16_t* gate, int packed, void* stream) {
+    KR_REQUIRE(packed >= 0 && packed <= 2, "kr_det_matmul_i8: packed must be 0, 1 or 2");
     kr_gemm_args g{};
     g.A = reinterpret_cast<const kr_half*>(xq);
     g.lda = K;
@@ -97,6 +90,7 @@ int kr_det_matmul_i8(const int8_t* xq, const float* sa, int M, int K, const int8
     g.N = N;
     g.K = K;
     g.a_frag = packed ? 1 : 0;
+    g.a_q16 = packed == 2 ? 1 : 0;
     g.i8 = 1;
     g.sa = sa;
     g.sw = sw;

@@ -108,3 +108,85 @@ def test_int8_epilogues(ep, packed):
         np.testing.assert_allclose(got.astype(np.float32), want.astype(np.float32), rtol=1e-3, atol=1e-3)
     else:
         assert np.array_equal(got, want)
+
+
+def _pack_f16(x16: torch.Tensor):
+    """fp16 [M, K] -> fragment-packed (kr_pack_fragments), rows padded to 16."""
+    M, K = x16.shape
+    out = torch.empty(_lib.lib().kr_fragment_bytes(M, K) // 2, dtype=torch.float16, device=DEV)
+    _lib.call("kr_pack_fragments", x16.data_ptr(), K, M, K, out.data_ptr(), _lib.stream_ptr())
+    return out
+
+
+def _activations(M, K, seed):
+    """fp16 rows of mixed magnitude, one all-zero row, one row of exact
+    halves (ties of x * inv), one with a single nonzero element."""
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(M, K, generator=g) * torch.rand(M, 1, generator=g).mul(20).add(1e-3)
+    if M > 3:
+        x[1] = 0
+        x[2] = (torch.arange(K) % 9 - 4).float() * 0.5
+        x[3] = 0
+        x[3, K // 3] = -7.25
+    return x.half()
+
+
+@pytest.mark.parametrize("M,K,N", [(1, 768, 768), (37, 768, 768), (256, 768, 768),
+                                   (256, 3072, 768), (300, 3072, 768), (512, 768, 3072),
+                                   (20, 256, 64)])
+def test_int8_matmul_quantised_on_load(M, K, N):
+    """packed = 2: fp16 fragment-packed activations quantised per row inside
+    the product (the decode path's output and value projections) == the
+    oracle's quantize_rows followed by the exact int8 product, bit for bit."""
+    x = _activations(M, K, M + K + N)
+    g = torch.Generator().manual_seed(N)
+    qw = torch.randint(-127, 128, (N, K), generator=g, dtype=torch.int8)
+    sw = torch.rand(N, generator=g) * 0.01 + 1e-4
+    qo, so = quant.quantize_rows(x.float().numpy())
+    want = quant.matmul_i8(qo, so, qw.numpy(), sw.numpy())
+    xf = _pack_f16(x.to(DEV))
+    wb = _pack_w(qw.to(DEV))
+    sw_d = sw.to(DEV)
+    out = torch.empty(M, N, dtype=torch.float32, device=DEV)
+    _lib.call("kr_det_matmul_i8", xf.data_ptr(), None, M, K, wb.data_ptr(), sw_d.data_ptr(), N,
+              out.data_ptr(), N, 0, None, None, 2, _lib.stream_ptr())
+    assert np.array_equal(out.cpu().numpy(), want)
+
+
+@pytest.mark.parametrize("ep", [4, 5])
+def test_int8_quantised_on_load_epilogues(ep):
+    """The residual and gated epilogues (output projection, value product) on
+    the packed = 2 path: equal to packed = 1 on kr_quantize_rows' output."""
+    M, K, N = 256, 3072 if ep == 5 else 768, 768
+    x = _activations(M, K, ep).to(DEV)
+    g = torch.Generator().manual_seed(11 * ep)
+    qw = torch.randint(-127, 128, (N, K), generator=g, dtype=torch.int8).to(DEV)
+    sw = (torch.rand(N, generator=g) * 1e-3).to(DEV)
+    res = torch.randn(M, N, generator=g).half().to(DEV)
+    gate = torch.rand(M, N, generator=g).half().to(DEV)
+    wb = _pack_w(qw)
+    q1, s1 = _quant_gpu(x, 1)
+    out1 = res.clone()
+    _lib.call("kr_det_matmul_i8", q1.data_ptr(), s1.data_ptr(), M, K, wb.data_ptr(), sw.data_ptr(),
+              N, out1.data_ptr(), N, ep, out1.data_ptr(), gate.data_ptr(), 1, _lib.stream_ptr())
+    xf = _pack_f16(x)
+    out2 = res.clone()
+    _lib.call("kr_det_matmul_i8", xf.data_ptr(), None, M, K, wb.data_ptr(), sw.data_ptr(), N,
+              out2.data_ptr(), N, ep, out2.data_ptr(), gate.data_ptr(), 2, _lib.stream_ptr())
+    assert torch.equal(out1, out2)
+    qo, so = quant.quantize_rows(x.float().cpu().numpy())
+    y = quant.matmul_i8(qo, so, qw.cpu().numpy(), sw.cpu().numpy())
+    want = _ref_epilogue(ep, y, res.cpu().numpy(), gate.cpu().numpy())
+    assert np.array_equal(out2.cpu().numpy(), want)
+
+
+def test_quantised_on_load_rejects_row_major():
+    """packed = 2 needs the fragment path: a large M is refused, not run."""
+    M, K, N = 600, 768, 768
+    x = torch.zeros(M, K, dtype=torch.float16, device=DEV)
+    w = torch.zeros(N, K, dtype=torch.int8, device=DEV)
+    sw = torch.ones(N, device=DEV)
+    out = torch.empty(M, N, dtype=torch.float32, device=DEV)
+    rc = _lib.lib().kr_det_matmul_i8(x.data_ptr(), None, M, K, w.data_ptr(), sw.data_ptr(), N,
+                                     out.data_ptr(), N, 0, None, None, 2, _lib.stream_ptr())
+    assert rc != 0

@@ -95,3 +95,50 @@ def test_rowgemm_order_and_row_invariance():
     for i in (0, 8, 36):
         np.testing.assert_array_equal(crc.gemm_rows(x[i:i + 1], W), y[i:i + 1])
     np.testing.assert_array_equal(crc.gemm_rows(x[5:30], W), y[5:30])
+
+
+def test_layer_norm_gpu_order_against_torch_and_closed_forms():
+    """oracle.rwkv4.layer_norm (the GPU row kernel's summation order) against
+    torch's layer_norm (float32, its own order) to float32 rounding, and two
+    rows whose result is fixed exactly: a constant row (mean exact, variance
+    0, so y = b exactly) and a row of +a / -a in equal numbers (mean 0
+    exactly, variance a^2 exactly for a power of two a, so y = +-(a * rstd)
+    * w + b with rstd = 1/sqrt(a^2 + 1e-5))."""
+    import torch.nn.functional as F
+    g = torch.Generator().manual_seed(5)
+    for C in (256, 768, 1024):
+        x = torch.randn(9, C, generator=g) * torch.rand(9, 1, generator=g).mul(8).add(0.01)
+        x[0] = 3.25
+        a = 0.5
+        x[1] = a * (1 - 2 * (torch.arange(C) % 2)).float()
+        w = torch.randn(C, generator=g).half().float()
+        b = torch.randn(C, generator=g).half().float()
+        y = rwkv4.layer_norm(x, w, b)
+        ref = F.layer_norm(x, (C,), w, b, rwkv4.LN_EPS)
+        np.testing.assert_allclose(y.numpy(), ref.numpy(), rtol=2e-5, atol=2e-5)
+        assert torch.equal(y[0], b)
+        f = np.float32
+        rstd = f(1.0) / np.sqrt(f(a * a) + f(rwkv4.LN_EPS))
+        sign = np.where(np.arange(C) % 2 == 0, f(1), f(-1))
+        want = (((sign * f(a)) * rstd).astype(f) * w.numpy()).astype(f) + b.numpy()
+        np.testing.assert_array_equal(y[1].numpy(), want.astype(f))
+
+
+def test_deterministic_sigmoid_and_wkv():
+    """The w8a8 codec's kexp-based sigmoid and WKV (fp16 mode of the int8
+    oracle) against torch's sigmoid and the WKV closed form, to float32
+    rounding; the sigmoid's two branches meet at 0 (0.5 exactly) and are
+    symmetric: s(-x) = 1 - s(x) within one rounding."""
+    x = torch.linspace(-30, 30, 4001)
+    s = rwkv4._sigmoid(x, True)
+    np.testing.assert_allclose(s.numpy(), torch.sigmoid(x).numpy(), rtol=3e-7, atol=1e-7)
+    assert float(rwkv4._sigmoid(torch.zeros(1), True)[0]) == 0.5
+    np.testing.assert_allclose((s + rwkv4._sigmoid(-x, True)).numpy(), 1.0, atol=1.2e-7)
+    g = torch.Generator().manual_seed(2)
+    B, T, C = 2, 30, 16
+    k = torch.randn(B, T, C, generator=g) * 2
+    v = torch.randn(B, T, C, generator=g)
+    w = -torch.exp(torch.linspace(-5, 3, C))
+    u = torch.full((C,), float(np.log(0.3)))
+    y = rwkv4.wkv(k, v, w, u, rwkv4.new_state(1, B, C)[0], det=True)
+    np.testing.assert_allclose(y.numpy(), _direct_wkv(k, v, w, u).numpy(), rtol=2e-5, atol=2e-6)
