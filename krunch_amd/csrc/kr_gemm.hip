@@ -558,9 +558,11 @@ __global__ void __launch_bounds__(MAXT) gemm_panel_kernel(kr_gemm_multi mj) {
     const int last_mb = (g.M - 1) >> 4, last_nb = (g.N - 1) >> 4;
     const long long lda16 = I8 ? g.lda >> 1 : g.lda, ldw16 = I8 ? g.ldw >> 1 : g.ldw;
 
-    // ---- operand loads: A once, W panels double buffered
+    // ---- operand loads: A once, W panels double buffered (int8: a panel is
+    // half the registers, so all NS panels are loaded up front)
+    constexpr int NB = I8 ? NS : 2;
     kr_half8 a[TM][QPS];
-    kr_half8 b[2][QPS];
+    kr_half8 b[NB][QPS];
     // QA: int8 block q of the slice holds, in lane (r, j) = (l % 16, l / 16),
     // the 16 halves k = 64q + 16j .. +15 of row r: fp16 block 2q + j/2 of the
     // slice, lanes r + 32(j % 2) and r + 32(j % 2) + 16.
@@ -603,8 +605,8 @@ __global__ void __launch_bounds__(MAXT) gemm_panel_kernel(kr_gemm_multi mj) {
             for (int q = 0; q < QPS; q++) a[i][q] = *reinterpret_cast<const kr_half8*>(ap + 32 * q);
         }
     }
-    load_w(0, b[0]);
-    if constexpr (NS > 1) load_w(1, b[1]);
+    #pragma unroll
+    for (int t = 0; t < (NB < NS ? NB : NS); t++) load_w(t, b[t]);
 
     // ---- epilogue operands of this wave's tiles (t = s, s + S, ...), fetched
     // behind the operand loads. The vector path needs 4-column groups that
@@ -700,14 +702,14 @@ __global__ void __launch_bounds__(MAXT) gemm_panel_kernel(kr_gemm_multi mj) {
             #pragma unroll
             for (int q = 0; q < QPS; q++) {
                 if constexpr (I8)
-                    p[i][t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(as_i4(b[t & 1][q]),
+                    p[i][t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(as_i4(b[t % NB][q]),
                                                                    as_i4(a[i][q]), p[i][t], 0, 0, 0);
                 else
-                    p[i][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(b[t & 1][q], a[i][q], p[i][t],
+                    p[i][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(b[t % NB][q], a[i][q], p[i][t],
                                                                     0, 0, 0);
             }
         }
-        if (t + 2 < NS) load_w(t + 2, b[t & 1]);
+        if (t + NB < NS) load_w(t + NB, b[t % NB]);
     }
     // int8: exact int32 sums dequantised once per output
     auto dequant = [&](int t, kr_int4 acc) -> kr_float4 {
@@ -847,8 +849,11 @@ int launch_panel(kr_gemm_multi mj, hipStream_t s) {
 // measured on MI355X at M = 256 they are 25-55% slower, so every wave keeps
 // all of its operand loads in flight at once. Taller tiles (TM = 4) keep
 // that property at K <= 1024, where the A fragments of 4 row blocks fit.
-constexpr PanelShape kShapes256[] = {{1, 1}, {1, 2}, {2, 1}, {2, 2}, {4, 1}, {4, 2}};
-constexpr PanelShape kShapes768[] = {{1, 1}, {1, 2}, {2, 1}, {2, 2}};
+// int8 operands also take NS = 4 (four int8 panels hold the registers of two
+// fp16 ones, all in flight at once).
+constexpr PanelShape kShapes256[] = {{1, 1}, {1, 2}, {2, 1}, {2, 2}, {4, 1}, {4, 2},
+                                     {1, 4}, {2, 4}};
+constexpr PanelShape kShapes768[] = {{1, 1}, {1, 2}, {2, 1}, {2, 2}, {1, 4}};
 constexpr PanelShape kShapes1024[] = {{1, 1}, {1, 2}};
 
 // Busiest-CU operand bytes (in 128-byte lines) for a shape: workgroups are
@@ -862,8 +867,13 @@ long long panel_cost(const kr_gemm_multi& mj, PanelShape sh) {
         wgs += (long long)((g.M + 16 * sh.TM - 1) / (16 * sh.TM)) *
                ((g.N + 16 * sh.NS - 1) / (16 * sh.NS));
     }
-    // QA with 4 row blocks needs more registers than a wave has (spills)
-    if (mj.job[0].a_q16 && sh.TM > 2) return LLONG_MAX;
+    // QA: each workgroup quantises its rows over the whole K, and every column
+    // group repeats that for the same rows, so one row block per workgroup
+    // (measured on MI355X at M = 256: the value product 7.4 us at TM 1 x NS 4
+    // against 8.8 at 2 x 2, the output projection 5.2 against 5.9);
+    // 4 panels only for int8 weights
+    if (mj.job[0].a_q16 && sh.TM > 1) return LLONG_MAX;
+    if (!mj.job[0].i8 && sh.NS > 2) return LLONG_MAX;
     const int ta = mj.job[0].a_q16 ? 2 * sh.TM : sh.TM;
     const long long per_wg = (long long)(ta + sh.NS) * mj.job[0].K / 4;
     return ((wgs + 255) / 256) * per_wg * 4096 - std::min<long long>(wgs, 256);
@@ -893,10 +903,14 @@ int launch_best(const kr_gemm_multi& mj, const PanelShape (&shapes)[N], hipStrea
 #define KR_PANEL(TM_, NS_) \
     if (best.TM == TM_ && best.NS == NS_) return launch_panel<TM_, NS_, FRAG, MAXT, I8, QA>(mj, s);
     if constexpr (MAXT == 256) {
-        KR_PANEL(1, 1) KR_PANEL(1, 2) KR_PANEL(2, 1) KR_PANEL(2, 2)
-        if constexpr (!QA) { KR_PANEL(4, 1) KR_PANEL(4, 2) }
+        KR_PANEL(1, 1) KR_PANEL(1, 2)
+        if constexpr (!QA) { KR_PANEL(2, 1) KR_PANEL(2, 2) KR_PANEL(4, 1) KR_PANEL(4, 2) }
+        if constexpr (I8) { KR_PANEL(1, 4) }
+        if constexpr (I8 && !QA) { KR_PANEL(2, 4) }
     } else if constexpr (MAXT == 768) {
-        KR_PANEL(1, 1) KR_PANEL(1, 2) KR_PANEL(2, 1) KR_PANEL(2, 2)
+        KR_PANEL(1, 1) KR_PANEL(1, 2)
+        if constexpr (!QA) { KR_PANEL(2, 1) KR_PANEL(2, 2) }
+        if constexpr (I8) { KR_PANEL(1, 4) }
     } else {
         KR_PANEL(1, 1) KR_PANEL(1, 2)
     }

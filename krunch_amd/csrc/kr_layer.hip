@@ -807,6 +807,22 @@ struct Phases {
     }
 };
 
+// Add the fragment-packed weight Wf ([N rows padded to 16] x K) to a staging
+// set, cut into the column groups of NS 16-column panels that the product
+// reading it will use; only when the groups are dealt to XCDs in eights.
+// elem: bytes per weight (2 fp16, 1 int8; a 16-row fragment row is 16*K*elem).
+void stage_weight(PrefetchSet& pf, const void* Wf, int N, int K, int NS, int elem = 2) {
+    // whole groups only (the buffer ends at the last one), dealt in eights
+    if (!Wf || NS <= 0 || pf.n >= 4 || N % (16 * NS) != 0 || (N / (16 * NS)) % 8 != 0) return;
+    const int groups = N / (16 * NS);
+    pf.base[pf.n] = static_cast<const char*>(Wf);
+    pf.group_bytes[pf.n] = (long long)NS * 16 * K * elem;
+    pf.n_groups[pf.n] = groups;
+    pf.n++;
+}
+
+constexpr int kStageBlocks = 512;   // staging workgroups per LN-mix launch (64 per XCD)
+
 // w8a8 layer: the same op order with the seven products on
 // int8 MFMA. LN-mix writes its operands quantised per row. On the small-M
 // fragment path the output projection and the channel-mix value product
@@ -869,9 +885,25 @@ int layer_forward_q8(const kr_layer_weights& L, int C, int F, kr_half* x, int B,
     a.run = rows_per_run(T);
     a.frag = fr ? 1 : 0;
     set_embed(a, e, x);
+    // stepped: LN1 stages the int8 K, V, R and output-projection weights in
+    // their XCDs' L2, LN2 the value product's (as layer_step_fused does)
+    PrefetchSet pf_ffn{};
+    if (fr && T == 1) {
+        const int ns_kvr = kKvrShapes[kvr_wkv_shape(G, M)][1];
+        stage_weight(a.pf, Q.K.qf, C, C, ns_kvr, 1);
+        stage_weight(a.pf, Q.V.qf, C, C, ns_kvr, 1);
+        stage_weight(a.pf, Q.R.qf, C, C, ns_kvr, 1);
+        const kr_gemm_args o = gemm_q8_q16(w.ry, M, C, Q.O, C, x, x);
+        stage_weight(a.pf, Q.O.qf, C, C, kr_gemm_panel_ns(&o, 1), 1);
+        a.pf.blocks = kStageBlocks;
+        const kr_gemm_args v = gemm_q8_q16(w.kf, M, F, Q.fV, C, x, x, w.rf);
+        stage_weight(pf_ffn, Q.fV.qf, C, F, kr_gemm_panel_ns(&v, 1), 1);
+        pf_ffn.blocks = kStageBlocks;
+    }
     KR_TRY(ph.mark(0));
     KR_TRY(launch_ln_mix<3>(G, a, s));
     set_embed(a, nullptr, x);
+    a.pf = pf_ffn;
     KR_TRY(ph.mark(1));
     if (fr && T == 1) {
         // stepped: the three int8 products and the WKV update in one launch
@@ -942,20 +974,6 @@ int layer_forward_q8(const kr_layer_weights& L, int C, int F, kr_half* x, int B,
 // Stepped (T = 1) fp16 layer with fragment-packed weights: LN1-mix, the
 // K, V, R products fused with WKV, the output projection, LN2-mix and the
 // channel mix (six launches).
-// Add the fragment-packed weight Wf ([N rows padded to 16] x K) to a staging
-// set, cut into the column groups of NS 16-column panels that the product
-// reading it will use; only when the groups are dealt to XCDs in eights.
-void stage_weight(PrefetchSet& pf, const void* Wf, int N, int K, int NS) {
-    // whole groups only (the buffer ends at the last one), dealt in eights
-    if (!Wf || NS <= 0 || pf.n >= 4 || N % (16 * NS) != 0 || (N / (16 * NS)) % 8 != 0) return;
-    const int groups = N / (16 * NS);
-    pf.base[pf.n] = static_cast<const char*>(Wf);
-    pf.group_bytes[pf.n] = (long long)NS * (K / 32) * 1024;
-    pf.n_groups[pf.n] = groups;
-    pf.n++;
-}
-
-constexpr int kStageBlocks = 512;   // staging workgroups per LN-mix launch (64 per XCD)
 
 int layer_step_fused(const kr_layer_weights& L, int C, int F, kr_half* x, int B,
                      const kr_layer_state& st, const Work& w, hipStream_t s,
