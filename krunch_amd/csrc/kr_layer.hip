@@ -116,6 +116,15 @@ __device__ __forceinline__ void store_row(kr_half* __restrict__ p, int lane, con
     }
 }
 
+// kr_frag_index(row, col, C) as a row part (wave-uniform: the address stays
+// in scalar registers) plus a 32-bit column part.
+__device__ __forceinline__ size_t frag_row_base(size_t row, int C) {
+    return (row >> 4) * (size_t)(C >> 5) * 512 + (row & 15) * 8;
+}
+__device__ __forceinline__ unsigned frag_col_off(int col) {
+    return (unsigned)(col >> 5) * 512u + (unsigned)((col & 31) >> 3) * 128u + (unsigned)(col & 7);
+}
+
 // Row `row` of a fragment-packed [*, C] operand (kr_frag_index): the lane's
 // 4-column groups are 4 consecutive halves there too.
 template <int G>
@@ -127,7 +136,7 @@ __device__ __forceinline__ void store_row_frag(kr_half* __restrict__ out, size_t
         kr_half4 h;
         #pragma unroll
         for (int q = 0; q < 4; q++) h[q] = kr_f16(r.v[i][q]);
-        *reinterpret_cast<kr_half4*>(out + kr_frag_index((long long)row, 256 * i + 4 * lane, C)) = h;
+        *reinterpret_cast<kr_half4*>(out + frag_row_base(row, C) + frag_col_off(256 * i + 4 * lane)) = h;
     }
 }
 
@@ -148,36 +157,40 @@ __device__ __forceinline__ void store_mix(kr_half* __restrict__ out, size_t row,
             h[q] = kr_f16(cur.v[i][q] * m + prev.v[i][q] * (1.0f - m));
         }
         const int col = 256 * i + 4 * lane;
-        const size_t o = frag ? kr_frag_index((long long)row, col, C) : row * C + col;
-        *reinterpret_cast<kr_half4*>(out + o) = h;
+        kr_half* base = out + (frag ? frag_row_base(row, C) : row * C);
+        *reinterpret_cast<kr_half4*>(base + (frag ? frag_col_off(col) : (unsigned)col)) = h;
     }
 }
 
 // w8a8: the fp16 mix row quantised per row by the rule of kr_quantize_rows
-// (kr_gemm.h), row-major or fragment-packed for the small-M int8 GEMM.
+// (kr_gemm.h), row-major or fragment-packed for the small-M int8 GEMM. The
+// mixes are held as fp16 while the row maximum is reduced (half the
+// registers of fp32 copies; LN-mix occupancy matters, see ln_mix_kernel).
 template <int G>
 __device__ __forceinline__ void store_mix_q8(int8_t* __restrict__ out, float* __restrict__ scales,
                                              size_t row, bool frag, const CoefH<G>& tm, int lane,
                                              const RowF<G>& cur, const RowF<G>& prev) {
     constexpr int C = 256 * G;
-    float v[G][4];
+    kr_half4 h[G];
     float amax = 0.0f;
     #pragma unroll
     for (int i = 0; i < G; i++)
         #pragma unroll
         for (int q = 0; q < 4; q++) {
             const float m = (float)tm.v[i][q];
-            v[i][q] = (float)kr_f16(cur.v[i][q] * m + prev.v[i][q] * (1.0f - m));
-            amax = fmaxf(amax, fabsf(v[i][q]));
+            h[i][q] = kr_f16(cur.v[i][q] * m + prev.v[i][q] * (1.0f - m));
+            amax = fmaxf(amax, fabsf((float)h[i][q]));
         }
     amax = kr_wave_reduce(amax, [](float a, float b) { return fmaxf(a, b); });
     const float inv = kr_q8_inv(amax);
     #pragma unroll
     for (int i = 0; i < G; i++) {
-        const uint32_t w = kr_q8_pack4(v[i][0], v[i][1], v[i][2], v[i][3], inv);
+        const uint32_t w = kr_q8_pack4((float)h[i][0], (float)h[i][1], (float)h[i][2],
+                                       (float)h[i][3], inv);
         const int col = 256 * i + 4 * lane;
-        const size_t o = frag ? kr_frag_index_i8((long long)row, col, C) : row * C + col;
-        *reinterpret_cast<uint32_t*>(out + o) = w;
+        // kr_frag_index_i8 (col even): twice the 16-bit view's index
+        int8_t* base = out + (frag ? 2 * frag_row_base(row, C / 2) : row * C);
+        *reinterpret_cast<uint32_t*>(base + (frag ? 2 * frag_col_off(col / 2) : (unsigned)col)) = w;
     }
     if (lane == 0) scales[row] = kr_q8_scale(amax);
 }
@@ -259,8 +272,19 @@ __device__ void prefetch_panels(const PrefetchSet& pf, int p) {
 // coefficient and the first rows are loaded before any store, so a T = 1
 // row costs one memory round trip.
 // NMIX == 0: plain LayerNorm into out[0] (ln_out before the head).
-template <int G, int NMIX>
-__global__ void __launch_bounds__(256) ln_mix_kernel(LnMixArgs a) {
+// Q8: the w8a8 form (mixes quantised into a.q[]), its own instantiation.
+// At least 3 waves per SIMD (<= 168 registers) for C <= 768: the L2 staging
+// workgroups this kernel also runs need the occupancy. Measured on MI355X
+// (fp16 decode KB/s, one box, A/B twice): fp16 and int8 forms in one kernel
+// 1,737 (LN2 at 207 registers, 2 waves); split, no bound 1,818 (LN1 at 186);
+// split, 3 waves 1,874 (LN1 spilling 60 bytes); 4 waves 1,800 (116-byte
+// spills). With the row index wave-uniform and the fragment index split into
+// a uniform row part and a 32-bit column part (addresses in scalar
+// registers), every form fits 3 waves without spilling (fp16 156 / 130,
+// int8 168 / 148 registers): w8a8 decode 1,727 -> 1,886.
+template <int G, int NMIX, bool Q8>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(G <= 3 ? 3 : 1)))
+ln_mix_kernel(LnMixArgs a) {
     constexpr int C = 256 * G;
     constexpr int NM = NMIX > 0 ? NMIX : 1;
     if ((int)blockIdx.x >= a.ln_blocks) {   // staging workgroups (uniform per workgroup)
@@ -271,6 +295,8 @@ __global__ void __launch_bounds__(256) ln_mix_kernel(LnMixArgs a) {
     const int runs = (a.T + a.run - 1) / a.run;
     int gw = (blockIdx.x * blockDim.x + threadIdx.x) >> 6;
     if (a.one_row) gw = threadIdx.x < 64 ? (int)blockIdx.x : a.B * runs;
+    // wave-uniform: every row pointer then lives in scalar registers
+    gw = __builtin_amdgcn_readfirstlane(gw);
     if (gw >= a.B * runs) return;
     const int b = gw / runs, t0 = (gw % runs) * a.run;
     const int t1 = min(a.T, t0 + a.run);
@@ -311,7 +337,7 @@ __global__ void __launch_bounds__(256) ln_mix_kernel(LnMixArgs a) {
         } else {
             #pragma unroll
             for (int m = 0; m < NMIX; m++) {
-                if (a.q[0]) store_mix_q8<G>(a.q[m], a.qs[m], row0 + t, a.frag != 0, tm[m], lane, cur, prev);
+                if constexpr (Q8) store_mix_q8<G>(a.q[m], a.qs[m], row0 + t, a.frag != 0, tm[m], lane, cur, prev);
                 else store_mix<G>(a.out[m], row0 + t, a.frag != 0, tm[m], lane, cur, prev);
             }
             prev = cur;
@@ -652,13 +678,17 @@ int launch_ln_mix(int G, const LnMixArgs& a_in, hipStream_t s) {
     a.ln_blocks = (int)((a.one_row ? waves : (waves + 3) / 4) + 7) / 8 * 8;
     if (a.pf.n == 0) a.pf.blocks = 0;
     const int blocks = a.ln_blocks + a.pf.blocks;
+    const bool q8 = NMIX > 0 && a.q[0] != nullptr;
+#define KR_LN(G_)                                                         \
+    case G_:                                                              \
+        if (q8) ln_mix_kernel<G_, NMIX, true><<<blocks, 256, 0, s>>>(a);  \
+        else ln_mix_kernel<G_, NMIX, false><<<blocks, 256, 0, s>>>(a);    \
+        break;
     switch (G) {
-        case 1: ln_mix_kernel<1, NMIX><<<blocks, 256, 0, s>>>(a); break;
-        case 2: ln_mix_kernel<2, NMIX><<<blocks, 256, 0, s>>>(a); break;
-        case 3: ln_mix_kernel<3, NMIX><<<blocks, 256, 0, s>>>(a); break;
-        case 4: ln_mix_kernel<4, NMIX><<<blocks, 256, 0, s>>>(a); break;
+        KR_LN(1) KR_LN(2) KR_LN(3) KR_LN(4)
         default: return kr_fail(KR_EUNSUPPORTED, "C=%d unsupported (256..1024, step 256)", 256 * G);
     }
+#undef KR_LN
     KR_LAUNCHED();
     return KR_OK;
 }
