@@ -412,19 +412,19 @@ def dominant_kernel_roofline(weights16, B):
 def step_kernel_bytes(B, C=768, F=3072, V=50277):
     h = 2
     return [
-        ("ln_mix_kernel<3, 3>", "LN1 + 3 mixes", 12,
+        ("ln_mix_kernel<3, 3, false>", "LN1 + 3 mixes", 12,
          6 * B * C * h + 5 * C * h),
-        ("kvr_wkv_kernel", "K, V, R products + WKV", 12,
+        ("kvr_wkv_kernel<3, 2, 2, false>", "K, V, R products + WKV", 12,
          3 * C * C * h + 3 * B * C * h + 2 * C * 4 + 2 * 3 * B * C * 4 + B * C * h),
-        ("gemm_panel_kernel<2, 2, true, 256", "output projection (residual)", 12,
+        ("gemm_panel_kernel<2, 2, true, 256, false", "output projection (residual)", 12,
          C * C * h + 4 * B * C * h),
-        ("ln_mix_kernel<3, 2>", "LN2 + 2 mixes", 12,
+        ("ln_mix_kernel<3, 2, false>", "LN2 + 2 mixes", 12,
          5 * B * C * h + 4 * C * h),
-        ("gemm_panel_kernel<4, 2, true, 256", "channel-mix R + K products", 12,
+        ("gemm_panel_kernel<4, 2, true, 256, false", "channel-mix R + K products", 12,
          (C + F) * C * h + 2 * B * C * h + B * (C + F) * h),
-        ("gemm_panel_kernel<2, 2, true, 768", "channel-mix value product (gated residual)", 12,
+        ("gemm_panel_kernel<2, 2, true, 768, false", "channel-mix value product (gated residual)", 12,
          C * F * h + B * F * h + 3 * B * C * h),
-        ("ln_mix_kernel<3, 0>", "LN_out", 1,
+        ("ln_mix_kernel<3, 0, false>", "LN_out", 1,
          2 * B * C * h + 2 * C * h),
         ("gemm_head_small_kernel", "head (M = B, N = V)", 1,
          V * C * h + B * C * h + B * V * h),
