@@ -874,6 +874,11 @@ long long panel_cost(const kr_gemm_multi& mj, PanelShape sh) {
     // 4 panels only for int8 weights
     if (mj.job[0].a_q16 && sh.TM > 1) return LLONG_MAX;
     if (!mj.job[0].i8 && sh.NS > 2) return LLONG_MAX;
+    // int8 operands: at most 2 row blocks (the stepped channel-mix R/K
+    // product at M = 256: w8a8 decode 1,880 -> 1,919 KB/s at 2 x 2 against
+    // 4 x 2, measured on MI355X; the fp16 product keeps 4 x 2, 1,883 against
+    // 1,878)
+    if (mj.job[0].i8 && sh.TM > 2) return LLONG_MAX;
     const int ta = mj.job[0].a_q16 ? 2 * sh.TM : sh.TM;
     const long long per_wg = (long long)(ta + sh.NS) * mj.job[0].K / 4;
     return ((wgs + 255) / 256) * per_wg * 4096 - std::min<long long>(wgs, 256);
