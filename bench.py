@@ -406,60 +406,88 @@ def dominant_kernel_roofline(weights16, B):
     return top, second
 
 
-# Algorithmic bytes of each kernel of one stepped decode step (B streams,
+# Algorithmic bytes of each phase of one stepped decode step (B streams,
 # C = 768, F = 3072, V = 50277, fp16 activations and weights, fp32 WKV
-# state), keyed by a substring of the kernel name; see DESIGN.md.
+# state); see DESIGN.md. Phase keys are assigned by step_phases.
 def step_kernel_bytes(B, C=768, F=3072, V=50277):
     h = 2
     return [
-        ("ln_mix_kernel<3, 3, false>", "LN1 + 3 mixes", 12,
-         6 * B * C * h + 5 * C * h),
-        ("kvr_wkv_kernel<3, 2, 2, false>", "K, V, R products + WKV", 12,
+        ("ln1", "LN1 + 3 mixes", 12, 6 * B * C * h + 5 * C * h),
+        ("kvr", "K, V, R products + WKV", 12,
          3 * C * C * h + 3 * B * C * h + 2 * C * 4 + 2 * 3 * B * C * 4 + B * C * h),
-        ("gemm_panel_kernel<2, 2, true, 256, false", "output projection (residual)", 12,
-         C * C * h + 4 * B * C * h),
-        ("ln_mix_kernel<3, 2, false>", "LN2 + 2 mixes", 12,
-         5 * B * C * h + 4 * C * h),
-        ("gemm_panel_kernel<4, 2, true, 256, false", "channel-mix R + K products", 12,
+        ("ow", "output projection (residual)", 12, C * C * h + 4 * B * C * h),
+        ("ln2", "LN2 + 2 mixes", 12, 5 * B * C * h + 4 * C * h),
+        ("rk", "channel-mix R + K products", 12,
          (C + F) * C * h + 2 * B * C * h + B * (C + F) * h),
-        ("gemm_panel_kernel<2, 2, true, 768, false", "channel-mix value product (gated residual)", 12,
+        ("fv", "channel-mix value product (gated residual)", 12,
          C * F * h + B * F * h + 3 * B * C * h),
-        ("ln_mix_kernel<3, 0, false>", "LN_out", 1,
-         2 * B * C * h + 2 * C * h),
-        ("gemm_head_small_kernel", "head (M = B, N = V)", 1,
-         V * C * h + B * C * h + B * V * h),
-        ("row_cdf_kernel<0, 4>", "softmax -> CDF -> range decode", 1,
-         B * V * h),
+        ("lnout", "LN_out", 1, 2 * B * C * h + 2 * C * h),
+        ("head", "head (M = B, N = V)", 1, V * C * h + B * C * h + B * V * h),
+        ("cdf", "softmax -> CDF -> range decode", 1, B * V * h),
     ]
 
 
+def step_phases(names):
+    """Phase key of each launch of a fp16 stepped decode, from the kernel
+    names in launch order (None for launches outside the decode step). The
+    tile shapes in the template arguments change with B, so the stepped
+    products are told apart by the launch before them: the output
+    projection follows the K/V/R+WKV launch, the channel-mix R + K product
+    follows LN2, the value product follows R + K."""
+    out, prev = [], None
+    for n in names:
+        if "ln_mix_kernel<3, 3, false>" in n:
+            ph = "ln1"
+        elif "ln_mix_kernel<3, 2, false>" in n:
+            ph = "ln2"
+        elif "ln_mix_kernel<3, 0, false>" in n:
+            ph = "lnout"
+        elif "kvr_wkv_kernel<" in n and ", false>" in n:
+            ph = "kvr"
+        elif "gemm_panel_kernel<" in n and "false, false>" in n:
+            ph = {"kvr": "ow", "ln2": "rk", "rk": "fv"}.get(prev)
+        elif "gemm_head_small_kernel" in n:
+            ph = "head"
+        elif "row_cdf_kernel<0, 4>" in n:
+            ph = "cdf"
+        else:
+            ph = None
+        out.append(ph)
+        prev = ph
+    return out
+
+
 def hbm_table(csv_path, B):
-    """Per-kernel HBM fraction of one decode step from a rocprofv3 kernel
-    trace of the bench (markdown on stdout): each kernel's algorithmic bytes
-    per launch over its average duration in the trace's decode steps
-    (the most frequent grid of that kernel), against 8 TB/s."""
+    """Per-phase HBM fraction of one decode step from a rocprofv3 kernel
+    trace of the bench (markdown on stdout): each phase's algorithmic bytes
+    per launch over its median duration in the trace's decode steps (the
+    most frequent kernel and grid of that phase), against 8 TB/s."""
     import csv
     import gzip
     opener = gzip.open if csv_path.endswith(".gz") else open
-    durs = {}
+    rows = []
     with opener(csv_path, "rt") as f:
         for r in csv.DictReader(f):
-            key = (r["Kernel_Name"], int(r["Grid_Size_X"]))
-            durs.setdefault(key, []).append(
-                (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1000.0)
+            rows.append((int(r["Start_Timestamp"]), int(r["End_Timestamp"]), r["Kernel_Name"],
+                         int(r["Grid_Size_X"])))
+    rows.sort()
+    durs = {}
+    for (t0, t1, name, grid), ph in zip(rows, step_phases([r[2] for r in rows])):
+        if ph is not None:
+            durs.setdefault(ph, {}).setdefault((name, grid), []).append((t1 - t0) / 1000.0)
     print(f"| kernel | phase | launches / step | avg us | algorithmic MB / launch | GB/s | "
           f"fraction of 8 TB/s | us / step |")
     print("|---|---|---|---|---|---|---|---|")
     total = 0.0
-    for sub, phase, per_step, nbytes in step_kernel_bytes(B):
-        cands = [(len(v), k) for k, v in durs.items() if sub in k[0]]
-        if not cands:
+    for key, phase, per_step, nbytes in step_kernel_bytes(B):
+        if key not in durs:
             continue
-        _, key = max(cands)
-        us = sorted(durs[key])[len(durs[key]) // 2]       # median launch
+        kn = max(durs[key], key=lambda k: len(durs[key][k]))
+        d = sorted(durs[key][kn])
+        us = d[len(d) // 2]                                  # median launch
         gbs = nbytes / (us * 1e-6) / 1e9
         total += us * per_step
-        name = key[0].replace("(anonymous namespace)::", "").replace("void ", "").split("(")[0]
+        name = kn[0].replace("(anonymous namespace)::", "").replace("void ", "").split("(")[0]
         print(f"| `{name}` | {phase} | {per_step} | {us:.2f} | {nbytes / 1e6:.2f} | {gbs:.0f} | "
               f"{gbs / (MI355X_HBM_PEAK / 1e9):.3f} | {us * per_step:.1f} |")
     print(f"\nSum over the step: {total:.1f} us (median launches; the profiler adds ~1 us per "

@@ -62,6 +62,11 @@ def test_config2_packed_B64_T1024_vs_oracle(eng, w16):
     assert err < 1e-2, f"config 2 logits vs fp32 oracle: max abs {err}"
     for i, b in enumerate(sel):
         _check_payload(enc[b], got[i], toks[b])
+        # bits/token within 0.5% of the fp32 oracle's own chain (its logits,
+        # its CDF, its coder) on the same stream
+        ref_bits = 8 * len(orc.encode(osm.logits_to_cdf(ref[i]), toks[b]))
+        gpu_bits = 8 * (len(enc[b]) - 8)
+        assert abs(gpu_bits - ref_bits) / ref_bits < 0.005, (b, gpu_bits / T, ref_bits / T)
 
 
 def test_config3_stepped_B128_1024_steps(eng):
