@@ -2,6 +2,8 @@
 and decompress them in lockstep (fused decode, HIP graph). Byte-exact round
 trips; the bitstream equals the oracle coder fed the oracle CDF of the GPU
 logits; bits/token within 0.5% of the fp32 oracle's."""
+import struct
+
 import numpy as np
 import pytest
 import torch
@@ -118,6 +120,27 @@ def test_bitstream_equals_oracle_chain(eng):
     for b in range(2):
         ref = orc.encode(osm.logits_to_cdf(logits[b]), toks[b])
         assert enc[b][8:] == ref
+
+
+def test_chunk_payloads_equal_oracle_chain(eng):
+    """Byte-level chunks (reference inference.py:576-660 compress_chunks_batched):
+    each payload is the ">II" (orig_len, n_tokens) mini-header and then the
+    oracle coder's bits on the oracle CDF of the GPU logits of the chunk's
+    byte-tokenized stream; ragged chunks share one batched call."""
+    from krunch_amd.tokenizer import ByteTokenizer
+    chunks = [b"The quick brown fox jumps over the lazy dog. " * 3,
+              bytes(range(200)), "Grüße, 世界!".encode("utf-8") * 5, b"x"]
+    enc = eng.compress_chunks_batched(chunks)
+    assert eng.decompress_chunks_batched(enc) == chunks
+    tok = ByteTokenizer()
+    W = eng.weights
+    for c, e in zip(chunks, enc):
+        ids = tok.encode_bytes(c)
+        assert struct.unpack(">II", e[:8]) == (len(c), len(ids))
+        st = cpp_path.fresh_state_batched(W, 1)
+        logits = cpp_path.forward_packed_batched(W, synthetic.model_inputs(ids[None, :]), st)
+        logits = logits.view(len(ids), -1).cpu().numpy()
+        assert e[8:] == orc.encode(osm.logits_to_cdf(logits), ids)
 
 
 def test_bits_per_token_close_to_fp32_oracle(eng):
