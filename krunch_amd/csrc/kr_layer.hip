@@ -360,7 +360,7 @@ ln_mix_kernel(LnMixArgs a) {
 // ry = fp16(r * fp16(y)), written row-major or fragment-packed (ry_frag) for
 // the output projection. State aa, bb, pp is read once and written once.
 // ---------------------------------------------------------------------------
-constexpr int kWkvChunk = 8;
+constexpr int kWkvChunk = 16;
 
 struct WkvState {
     float a, b, p;
@@ -399,28 +399,29 @@ __global__ void __launch_bounds__(256) wkv_kernel(const float* __restrict__ k,
     if (c >= C || b >= B) return;
     const size_t s = (size_t)b * C + c;
     const size_t base = (size_t)b * T * C + c;
-    // token 0 and every operand it needs are loaded together (T >= 1)
     const float w = decay[c], u = first[c];
     WkvState st{aa[s], bb[s], pp[s]};
-    const float k0 = k[base], v0 = v[base], r0 = (float)r[base];
     auto ry_at = [&](int t) -> size_t {
         return ry_frag ? kr_frag_index((long long)b * T + t, c, C) : base + (size_t)t * C;
     };
-    ry[ry_at(0)] = wkv_token<DET>(st, w, u, k0, v0, r0);
-    for (int t0 = 1; t0 < T; t0 += kWkvChunk) {
-        float kk[kWkvChunk], vv[kWkvChunk], rr[kWkvChunk];
+    // A chunk's loads are unconditional (tokens past T re-read token T-1) and
+    // r stays fp16 until its token is computed, so all 3 x kWkvChunk loads are
+    // in flight at once. A load under `t < T` with its conversion beside it
+    // makes the compiler wait for each token's loads in turn (one memory
+    // latency per token).
+    for (int t0 = 0; t0 < T; t0 += kWkvChunk) {
+        float kk[kWkvChunk], vv[kWkvChunk];
+        kr_half rh[kWkvChunk];
         #pragma unroll
         for (int q = 0; q < kWkvChunk; q++) {
-            if (t0 + q < T) {
-                const size_t i = base + (size_t)(t0 + q) * C;
-                kk[q] = k[i];
-                vv[q] = v[i];
-                rr[q] = (float)r[i];
-            }
+            const size_t i = base + (size_t)min(t0 + q, T - 1) * C;
+            kk[q] = k[i];
+            vv[q] = v[i];
+            rh[q] = r[i];
         }
         #pragma unroll
         for (int q = 0; q < kWkvChunk; q++)
-            if (t0 + q < T) ry[ry_at(t0 + q)] = wkv_token<DET>(st, w, u, kk[q], vv[q], rr[q]);
+            if (t0 + q < T) ry[ry_at(t0 + q)] = wkv_token<DET>(st, w, u, kk[q], vv[q], (float)rh[q]);
     }
     aa[s] = st.a;
     bb[s] = st.b;
