@@ -46,6 +46,39 @@ __global__ void __launch_bounds__(256) row_quant_kernel(const kr_half* __restric
     if (lane == 0) scales[row] = kr_q8_scale(amax);
 }
 
+// K = 256 KI: the lane's KI groups are loaded together and kept in
+// registers, so a row costs one memory round trip (the loop above waits for
+// each load in turn and reads the row twice). Same operations, same bits.
+template <int KI>
+__global__ void __launch_bounds__(256) row_quant_reg_kernel(const kr_half* __restrict__ x,
+                                                            long long ldx, int M,
+                                                            int8_t* __restrict__ q,
+                                                            float* __restrict__ scales, int packed) {
+    constexpr int K = 256 * KI;
+    const int lane = threadIdx.x & 63;
+    const int row = (blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+    if (row >= M) return;
+    const kr_half* xr = x + (size_t)row * (size_t)ldx;
+    kr_half4 h[KI];
+    #pragma unroll
+    for (int i = 0; i < KI; i++) h[i] = *reinterpret_cast<const kr_half4*>(xr + 256 * i + 4 * lane);
+    float amax = 0.0f;
+    #pragma unroll
+    for (int i = 0; i < KI; i++)
+        #pragma unroll
+        for (int r = 0; r < 4; r++) amax = fmaxf(amax, fabsf((float)h[i][r]));
+    amax = wave_maxf(amax);
+    const float inv = kr_q8_inv(amax);
+    #pragma unroll
+    for (int i = 0; i < KI; i++) {
+        const int c = 256 * i + 4 * lane;
+        const size_t o = packed ? kr_frag_index_i8(row, c, K) : (size_t)row * (size_t)K + c;
+        *reinterpret_cast<uint32_t*>(q + o) =
+            kr_q8_pack4((float)h[i][0], (float)h[i][1], (float)h[i][2], (float)h[i][3], inv);
+    }
+    if (lane == 0) scales[row] = kr_q8_scale(amax);
+}
+
 }  // namespace
 
 int kr_impl_quantize_rows(const void* x, long long ldx, int M, int K, void* q, float* scales,
@@ -54,8 +87,16 @@ int kr_impl_quantize_rows(const void* x, long long ldx, int M, int K, void* q, f
                "quantize: bad args (K must be a multiple of 64)");
     KR_REQUIRE(((uintptr_t)x & 7) == 0 && ((uintptr_t)q & 3) == 0, "quantize: misaligned pointer");
     if (M == 0) return KR_OK;
-    row_quant_kernel<<<(M + 3) / 4, 256, 0, s>>>(reinterpret_cast<const kr_half*>(x), ldx, M, K,
-                                                 reinterpret_cast<int8_t*>(q), scales, packed);
+    const kr_half* xh = reinterpret_cast<const kr_half*>(x);
+    int8_t* q8 = reinterpret_cast<int8_t*>(q);
+    const int grid = (M + 3) / 4;
+    switch (K % 256 == 0 ? K / 256 : 0) {
+#define KR_RQ(KI_) \
+        case KI_: row_quant_reg_kernel<KI_><<<grid, 256, 0, s>>>(xh, ldx, M, q8, scales, packed); break;
+        KR_RQ(1) KR_RQ(2) KR_RQ(3) KR_RQ(4) KR_RQ(6) KR_RQ(8) KR_RQ(12)
+#undef KR_RQ
+        default: row_quant_kernel<<<grid, 256, 0, s>>>(xh, ldx, M, K, q8, scales, packed); break;
+    }
     KR_LAUNCHED();
     return KR_OK;
 }

@@ -29,7 +29,10 @@ def _pack_w(wq: torch.Tensor):
     return out
 
 
-@pytest.mark.parametrize("M,K", [(1, 768), (37, 768), (300, 3072), (16, 64)])
+# K = 256 KI (KI in 1..4, 6, 8, 12) takes the register-resident row kernel,
+# any other multiple of 64 the looping one
+@pytest.mark.parametrize("M,K", [(1, 768), (37, 768), (300, 3072), (16, 64), (9, 256), (5, 512),
+                                 (7, 1024), (3, 1536), (4, 2048), (6, 320)])
 def test_quantize_rows_matches_oracle(M, K):
     g = torch.Generator().manual_seed(M + K)
     x = (torch.randn(M, K, generator=g) * torch.rand(M, 1, generator=g) * 8).half()
