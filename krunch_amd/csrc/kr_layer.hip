@@ -235,16 +235,24 @@ struct LnMixArgs {
 // the compiler must keep, and nothing is stored. The 16-byte chunks XCD x
 // stages (all regions, groups x, x + 8, ...) are numbered in one sequence and
 // dealt over the XCD's staging threads, eight loads in flight per thread, so a
-// thread waits on memory about twice rather than once per group.
+// thread waits on memory about twice rather than once per group. The region
+// tables are read with constant indices only (kernel arguments in scalar
+// registers) and a chunk's region picked by selects: an array element at a
+// run-time index would be fetched from argument memory before every load,
+// and each of the eight loads would wait for the one before.
 __device__ void prefetch_panels(const PrefetchSet& pf, int p) {
     const int x = p & 7, nr = pf.blocks >> 3;
     const int t = (p >> 3) * 256 + (int)threadIdx.x, T = nr * 256;
+    const char* base[4];
+    long long gb[4];
     int per[4], cum[5];
     cum[0] = 0;
     #pragma unroll
     for (int i = 0; i < 4; i++) {
+        base[i] = pf.base[i];
+        gb[i] = pf.group_bytes[i];
         const int groups_x = i < pf.n ? (pf.n_groups[i] - x + 7) / 8 : 0;   // groups x, x+8, ...
-        per[i] = i < pf.n ? (int)(pf.group_bytes[i] >> 4) : 1;             // chunks per group
+        per[i] = i < pf.n ? (int)(gb[i] >> 4) : 1;                         // chunks per group
         cum[i + 1] = cum[i] + groups_x * per[i];
     }
     unsigned acc = 0;
@@ -255,9 +263,14 @@ __device__ void prefetch_panels(const PrefetchSet& pf, int p) {
             const int c = c0 + u * T;
             v[u] = make_uint4(0, 0, 0, 0);
             if (c < cum[4]) {
-                const int i = c < cum[1] ? 0 : (c < cum[2] ? 1 : (c < cum[3] ? 2 : 3));
-                const int r = c - cum[i], gi = r / per[i], o = r - gi * per[i];
-                v[u] = reinterpret_cast<const uint4*>(pf.base[i] + (long long)(x + 8 * gi) * pf.group_bytes[i])[o];
+                // the region holding chunk c: the last one starting at or before it
+                const bool r1 = c >= cum[1], r2 = c >= cum[2], r3 = c >= cum[3];
+                const char* b = r3 ? base[3] : (r2 ? base[2] : (r1 ? base[1] : base[0]));
+                const long long g = r3 ? gb[3] : (r2 ? gb[2] : (r1 ? gb[1] : gb[0]));
+                const int pr = r3 ? per[3] : (r2 ? per[2] : (r1 ? per[1] : per[0]));
+                const int cs = r3 ? cum[3] : (r2 ? cum[2] : (r1 ? cum[1] : cum[0]));
+                const int r = c - cs, gi = r / pr, o = r - gi * pr;
+                v[u] = reinterpret_cast<const uint4*>(b + (long long)(x + 8 * gi) * g)[o];
             }
         }
         #pragma unroll
