@@ -339,8 +339,16 @@ ln_mix_kernel(LnMixArgs a) {
         to_float<G>(prev_h, prev);
         if (t0 != 0) layer_norm_row<G>(prev, w, bias);
     }
+    CoefH<G> next_h;
     for (int t = t0; t < t1; t++) {
-        if (t != t0) load_coef<G>(xrow(row0 + t), lane, first_h);
+        if constexpr (!Q8) {
+            // the next row in flight while this one is computed (runs of
+            // rows; the int8 form has no registers to spare for it)
+            if (t > t0) first_h = next_h;
+            if (t + 1 < t1) load_coef<G>(xrow(row0 + t + 1), lane, next_h);
+        } else {
+            if (t != t0) load_coef<G>(xrow(row0 + t), lane, first_h);
+        }
         if (a.ids) store_coef<G>(a.xw + (row0 + t) * C, lane, first_h);
         to_float<G>(first_h, cur);
         layer_norm_row<G>(cur, w, bias);
