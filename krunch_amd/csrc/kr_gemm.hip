@@ -849,11 +849,13 @@ int launch_panel(kr_gemm_multi mj, hipStream_t s) {
 // measured on MI355X at M = 256 they are 25-55% slower, so every wave keeps
 // all of its operand loads in flight at once. Taller tiles (TM = 4) keep
 // that property at K <= 1024, where the A fragments of 4 row blocks fit.
-// int8 operands also take NS = 4 (four int8 panels hold the registers of two
-// fp16 ones, all in flight at once).
+// int8 operands also take NS = 3 and 4 (four int8 panels hold the registers
+// of two fp16 ones, all in flight at once). At M = 256 and N = 768, NS = 3
+// makes 16 column groups: one workgroup per CU, and a multiple of 8, so the
+// XCD dealing and L2 staging apply (w8a8 decode +2.8% against NS = 4).
 constexpr PanelShape kShapes256[] = {{1, 1}, {1, 2}, {2, 1}, {2, 2}, {4, 1}, {4, 2},
-                                     {1, 4}, {2, 4}};
-constexpr PanelShape kShapes768[] = {{1, 1}, {1, 2}, {2, 1}, {2, 2}, {1, 4}};
+                                     {1, 4}, {2, 4}, {1, 3}, {2, 3}};
+constexpr PanelShape kShapes768[] = {{1, 1}, {1, 2}, {2, 1}, {2, 2}, {1, 4}, {1, 3}};
 constexpr PanelShape kShapes1024[] = {{1, 1}, {1, 2}};
 
 // Busiest-CU operand bytes (in 128-byte lines) for a shape: workgroups are
@@ -910,12 +912,12 @@ int launch_best(const kr_gemm_multi& mj, const PanelShape (&shapes)[N], hipStrea
     if constexpr (MAXT == 256) {
         KR_PANEL(1, 1) KR_PANEL(1, 2)
         if constexpr (!QA) { KR_PANEL(2, 1) KR_PANEL(2, 2) KR_PANEL(4, 1) KR_PANEL(4, 2) }
-        if constexpr (I8) { KR_PANEL(1, 4) }
-        if constexpr (I8 && !QA) { KR_PANEL(2, 4) }
+        if constexpr (I8) { KR_PANEL(1, 4) KR_PANEL(1, 3) }
+        if constexpr (I8 && !QA) { KR_PANEL(2, 4) KR_PANEL(2, 3) }
     } else if constexpr (MAXT == 768) {
         KR_PANEL(1, 1) KR_PANEL(1, 2)
         if constexpr (!QA) { KR_PANEL(2, 1) KR_PANEL(2, 2) }
-        if constexpr (I8) { KR_PANEL(1, 4) }
+        if constexpr (I8) { KR_PANEL(1, 4) KR_PANEL(1, 3) }
     } else {
         KR_PANEL(1, 1) KR_PANEL(1, 2)
     }
