@@ -558,9 +558,9 @@ __global__ void __launch_bounds__(MAXT) gemm_panel_kernel(kr_gemm_multi mj) {
     const int last_mb = (g.M - 1) >> 4, last_nb = (g.N - 1) >> 4;
     const long long lda16 = I8 ? g.lda >> 1 : g.lda, ldw16 = I8 ? g.ldw >> 1 : g.ldw;
 
-    // ---- operand loads: A once, W panels double buffered (int8: a panel is
-    // half the registers, so all NS panels are loaded up front)
-    constexpr int NB = I8 ? NS : 2;
+    // ---- operand loads: A once, W panels double buffered (int8, and fp16
+    // with three panels of one row block: all NS panels loaded up front)
+    constexpr int NB = (I8 || NS == 3) ? NS : 2;
     kr_half8 a[TM][QPS];
     kr_half8 b[NB][QPS];
     // QA: int8 block q of the slice holds, in lane (r, j) = (l % 16, l / 16),
@@ -850,9 +850,11 @@ int launch_panel(kr_gemm_multi mj, hipStream_t s) {
 // all of its operand loads in flight at once. Taller tiles (TM = 4) keep
 // that property at K <= 1024, where the A fragments of 4 row blocks fit.
 // int8 operands also take NS = 3 and 4 (four int8 panels hold the registers
-// of two fp16 ones, all in flight at once). At M = 256 and N = 768, NS = 3
-// makes 16 column groups: one workgroup per CU, and a multiple of 8, so the
-// XCD dealing and L2 staging apply (w8a8 decode +2.8% against NS = 4).
+// of two fp16 ones, all in flight at once), and one-row-block fp16 tiles
+// NS = 3 with all three panels loaded up front. At M = 256 and N = 768,
+// NS = 3 makes 16 column groups: one workgroup per CU, and a multiple of 8,
+// so the XCD dealing and L2 staging apply (measured on MI355X: w8a8 decode
+// +2.8% against 1 x 4, fp16 decode +0.9% against 2 x 2).
 constexpr PanelShape kShapes256[] = {{1, 1}, {1, 2}, {2, 1}, {2, 2}, {4, 1}, {4, 2},
                                      {1, 4}, {2, 4}, {1, 3}, {2, 3}};
 constexpr PanelShape kShapes768[] = {{1, 1}, {1, 2}, {2, 1}, {2, 2}, {1, 4}, {1, 3}};
@@ -875,7 +877,7 @@ long long panel_cost(const kr_gemm_multi& mj, PanelShape sh) {
     // against 8.8 at 2 x 2, the output projection 5.2 against 5.9);
     // 4 panels only for int8 weights
     if (mj.job[0].a_q16 && sh.TM > 1) return LLONG_MAX;
-    if (!mj.job[0].i8 && sh.NS > 2) return LLONG_MAX;
+    if (!mj.job[0].i8 && sh.NS > 2 && !(sh.NS == 3 && sh.TM == 1)) return LLONG_MAX;
     // int8 operands: at most 2 row blocks (the stepped channel-mix R/K
     // product at M = 256: w8a8 decode 1,880 -> 1,919 KB/s at 2 x 2 against
     // 4 x 2, measured on MI355X; the fp16 product keeps 4 x 2, 1,883 against
@@ -912,12 +914,13 @@ int launch_best(const kr_gemm_multi& mj, const PanelShape (&shapes)[N], hipStrea
     if constexpr (MAXT == 256) {
         KR_PANEL(1, 1) KR_PANEL(1, 2)
         if constexpr (!QA) { KR_PANEL(2, 1) KR_PANEL(2, 2) KR_PANEL(4, 1) KR_PANEL(4, 2) }
-        if constexpr (I8) { KR_PANEL(1, 4) KR_PANEL(1, 3) }
+        KR_PANEL(1, 3)
+        if constexpr (I8) { KR_PANEL(1, 4) }
         if constexpr (I8 && !QA) { KR_PANEL(2, 4) KR_PANEL(2, 3) }
     } else if constexpr (MAXT == 768) {
-        KR_PANEL(1, 1) KR_PANEL(1, 2)
+        KR_PANEL(1, 1) KR_PANEL(1, 2) KR_PANEL(1, 3)
         if constexpr (!QA) { KR_PANEL(2, 1) KR_PANEL(2, 2) }
-        if constexpr (I8) { KR_PANEL(1, 4) KR_PANEL(1, 3) }
+        if constexpr (I8) { KR_PANEL(1, 4) }
     } else {
         KR_PANEL(1, 1) KR_PANEL(1, 2)
     }
