@@ -396,12 +396,12 @@ def dominant_kernel_roofline(weights16, B):
     del WV
     bytes_v = F * C * 2 + M * F * 2 + 3 * M * C * 2
     top = _roofline_entry(
-        "gemm_panel_kernel<4,2,frag,256> (stepped channel-mix R + K products in one launch, "
-        "M=%d K=768 N=768 sigmoid + 3072 relu^2; top kernel by time)" % M,
+        "gemm_panel_kernel (stepped channel-mix R + K products in one launch, "
+        "M=%d K=768 N=768 sigmoid + 3072 relu^2, fragment-packed operands; top kernel by time)" % M,
         bytes_rk, us_rk, "gemm_panel_ffn_rk_B256_traffic.json", B)
     second = _roofline_entry(
-        "gemm_panel_kernel<2,2,frag,768> (stepped channel-mix value product, M=%d K=3072 N=768, "
-        "gated residual; second by time)" % M,
+        "gemm_panel_kernel (stepped channel-mix value product, M=%d K=3072 N=768, "
+        "gated residual, fragment-packed operands; second by time)" % M,
         bytes_v, us_v, "gemm_panel_ffn_value_B256_traffic.json", B)
     return top, second
 
