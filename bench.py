@@ -412,7 +412,8 @@ def dominant_kernel_roofline(weights16, B):
 def step_kernel_bytes(B, C=768, F=3072, V=50277):
     h = 2
     return [
-        ("ln1", "LN1 + 3 mixes", 12, 6 * B * C * h + 5 * C * h),
+        # layer 0's LN1-mix of the next step runs in the decode kernel below
+        ("ln1", "LN1 + 3 mixes (layers 1-11)", 11, 6 * B * C * h + 5 * C * h),
         ("kvr", "K, V, R products + WKV", 12,
          3 * C * C * h + 3 * B * C * h + 2 * C * 4 + 2 * 3 * B * C * 4 + B * C * h),
         ("ow", "output projection (residual)", 12, C * C * h + 4 * B * C * h),
@@ -423,7 +424,8 @@ def step_kernel_bytes(B, C=768, F=3072, V=50277):
          C * F * h + B * F * h + 3 * B * C * h),
         ("lnout", "LN_out", 1, 2 * B * C * h + 2 * C * h),
         ("head", "head (M = B, N = V)", 1, V * C * h + B * C * h + B * V * h),
-        ("cdf", "softmax -> CDF -> range decode", 1, B * V * h),
+        ("cdf", "softmax -> CDF -> range decode + layer 0's LN1 + 3 mixes", 1,
+         B * V * h + 6 * B * C * h + 5 * C * h),
     ]
 
 

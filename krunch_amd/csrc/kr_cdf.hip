@@ -29,6 +29,7 @@
 
 #include "kr_math.h"
 #include "kr_rc_device.h"
+#include "kr_rowops.h"
 #include "kr_wave.h"
 
 namespace {
@@ -65,6 +66,7 @@ struct DecodeArgs {
     long long tok_stride;
     int32_t* tok_count;       // [B] tokens written so far (nullable)
     const int32_t* n_tokens;  // [B] stream length; finished streams are skipped (nullable)
+    const kr_embed_mix* em;   // layer 0's LN1-mix of the decoded token (device; nullable)
 };
 
 struct RowShared {
@@ -374,15 +376,21 @@ __device__ __forceinline__ void cdf_row(const void* __restrict__ input, long lon
         }
         StagedRow staged;
         pad = stage_row_load(reinterpret_cast<const kr_half*>(rowp), V, tid, staged);
-        // Finished streams do nothing this step (uniform per workgroup).
-        if (D.n_tokens && D.tok_count && D.tok_count[row] >= D.n_tokens[row]) return;
-        if (tid == 0) {
+        // Finished streams decode nothing this step (uniform per workgroup);
+        // layer 0 still takes their last symbol, as its own LN1-mix would
+        // (after the staged row has left the registers it holds).
+        const bool finished = D.n_tokens && D.tok_count && D.tok_count[row] >= D.n_tokens[row];
+        if (!finished && tid == 0) {
             uint32_t lim = D.in_len > o ? D.in_len - o : 0u;
             if (lim_cap < lim) lim = lim_cap;
             win.open(D.in + (o < D.in_len ? o : 0u), lim, dst.bit_offset);
         }
         copy_plan(P, sh, tid);
         stage_row_store(V, stage, tid, pad, staged);
+        if (finished) {
+            if (D.em && wave == 0) embed_mix(*D.em, (size_t)row, D.out_syms[row], lane);
+            return;
+        }
     }
 
     if constexpr (IN == IN_LOGITS_F16) {
@@ -715,6 +723,13 @@ __device__ __forceinline__ void cdf_row(const void* __restrict__ input, long lon
             }
         }
         __syncthreads();
+        if (D.em && wave >= 4) {
+            // layer 0's K, V, R and output projection weights into this XCD's
+            // L2 (workgroup row runs on XCD row % 8) while wave 0 searches
+            // and mixes: 3 staging blocks of 4 waves per row
+            const int k = (row >> 3) * 3 + ((wave - 4) >> 2);
+            if (k < (D.em->pf.blocks >> 3)) prefetch_panels(D.em->pf, 8 * k + (row & 7), tid & 255);
+        }
         if (wave == 0) {
             // Symbol search inside the hit leaf (<= 128 counts): two counts
             // per lane, an inclusive scan, and the first lane whose range
@@ -759,6 +774,7 @@ __device__ __forceinline__ void cdf_row(const void* __restrict__ input, long lon
                     if (D.tok_count) D.tok_count[row] = cnt + 1;
                 }
             }
+            if (D.em) embed_mix(*D.em, (size_t)row, s, lane);   // s is wave-uniform
         }
     }
 }
@@ -985,6 +1001,34 @@ int launch_rows(const void* in, long long ld, int N, int V, int prec, void* out,
 
 }  // namespace
 
+// kr_softmax_cdf_decode, plus (em non-null) layer 0's LN1-mix of each decoded
+// token; em is a device copy of a kr_embed_mix (kr_model.h) that
+// kr_impl_embed_mix_args filled.
+int kr_impl_cdf_decode(const uint16_t* logits, int B, int V, long long ld,
+                       const uint8_t* input_buf, uint32_t in_len,
+                       const int32_t* base_byte_offsets, const int32_t* byte_limits,
+                       uint32_t* states, int32_t* out_syms, int32_t* tokens,
+                       long long tok_stride, int32_t* tok_count, const int32_t* n_tokens,
+                       int cdf_precision, const kr_embed_mix* em, void* stream) {
+    KR_REQUIRE(logits && input_buf && states && out_syms, "kr_softmax_cdf_decode: null pointer");
+    KR_REQUIRE(ld >= V, "kr_softmax_cdf_decode: ld %lld < V %d", ld, V);
+    KR_REQUIRE(!tokens || tok_stride >= 1, "kr_softmax_cdf_decode: bad tok_stride");
+    DecodeArgs D;
+    D.in = input_buf;
+    D.in_len = in_len;
+    D.base = base_byte_offsets;
+    D.limits = byte_limits;
+    D.states = reinterpret_cast<kr_rc_state*>(states);
+    D.out_syms = out_syms;
+    D.tokens = tokens;
+    D.tok_stride = tok_stride;
+    D.tok_count = tok_count;
+    D.n_tokens = n_tokens;
+    D.em = em;
+    return launch_rows<IN_LOGITS_F16, M_DECODE>(logits, ld, B, V, cdf_precision, nullptr, 0,
+                                                nullptr, D, stream);
+}
+
 extern "C" {
 
 int kr_probs_to_cdf(const float* probs, int N, int V, long long ld, uint32_t* cdf_out,
@@ -1029,22 +1073,9 @@ int kr_softmax_cdf_decode(const uint16_t* logits, int B, int V, long long ld,
                           uint32_t* states, int32_t* out_syms, int32_t* tokens,
                           long long tok_stride, int32_t* tok_count, const int32_t* n_tokens,
                           int cdf_precision, void* stream) {
-    KR_REQUIRE(logits && input_buf && states && out_syms, "kr_softmax_cdf_decode: null pointer");
-    KR_REQUIRE(ld >= V, "kr_softmax_cdf_decode: ld %lld < V %d", ld, V);
-    KR_REQUIRE(!tokens || tok_stride >= 1, "kr_softmax_cdf_decode: bad tok_stride");
-    DecodeArgs D;
-    D.in = input_buf;
-    D.in_len = in_len;
-    D.base = base_byte_offsets;
-    D.limits = byte_limits;
-    D.states = reinterpret_cast<kr_rc_state*>(states);
-    D.out_syms = out_syms;
-    D.tokens = tokens;
-    D.tok_stride = tok_stride;
-    D.tok_count = tok_count;
-    D.n_tokens = n_tokens;
-    return launch_rows<IN_LOGITS_F16, M_DECODE>(logits, ld, B, V, cdf_precision, nullptr, 0,
-                                                nullptr, D, stream);
+    return kr_impl_cdf_decode(logits, B, V, ld, input_buf, in_len, base_byte_offsets, byte_limits,
+                              states, out_syms, tokens, tok_stride, tok_count, n_tokens,
+                              cdf_precision, nullptr, stream);
 }
 
 }  // extern "C"

@@ -21,7 +21,15 @@ int kr_impl_forward_layers(const kr_model_weights* m, void* x, int B, int T, voi
                            void* ws, size_t ws_bytes, hipStream_t s, const int32_t* ids);
 int kr_impl_forward_layers_view(const kr_model_weights* m, void* x, int B, int T, void* state,
                                 int state_B, int b0, void* ws, size_t ws_bytes, hipStream_t s,
-                                const int32_t* ids);
+                                const int32_t* ids, bool l0_mixed);
+bool kr_impl_embed_mix_args(const kr_model_weights* m, int B, void* state, int state_B, int b0,
+                            void* ws, void* x, bool first, kr_embed_mix* em, kr_embed_mix** dev);
+int kr_impl_cdf_decode(const uint16_t* logits, int B, int V, long long ld,
+                       const uint8_t* input_buf, uint32_t in_len,
+                       const int32_t* base_byte_offsets, const int32_t* byte_limits,
+                       uint32_t* states, int32_t* out_syms, int32_t* tokens,
+                       long long tok_stride, int32_t* tok_count, const int32_t* n_tokens,
+                       int cdf_precision, const kr_embed_mix* em, void* stream);
 int kr_impl_embed(const kr_model_weights* m, const int32_t* ids, int M, void* x, hipStream_t s);
 // xn_rows16: xn holds M rounded up to 16 rows (allows the small-M head).
 int kr_impl_head(const kr_model_weights* m, const void* x, int M, void* xn, void* logits,
@@ -33,12 +41,6 @@ extern "C" {
 int kr_softmax_cdf_pairs(const uint16_t* logits, int N, int V, long long ld,
                          const int32_t* symbols, uint32_t* pairs, int cdf_precision,
                          void* stream);
-int kr_softmax_cdf_decode(const uint16_t* logits, int B, int V, long long ld,
-                          const uint8_t* input_buf, uint32_t in_len,
-                          const int32_t* base_byte_offsets, const int32_t* byte_limits,
-                          uint32_t* states, int32_t* out_syms, int32_t* tokens,
-                          long long tok_stride, int32_t* tok_count, const int32_t* n_tokens,
-                          int cdf_precision, void* stream);
 int kr_probs_to_cdf(const float* probs, int N, int V, long long ld, uint32_t* cdf_out,
                     int cdf_precision, void* stream);
 }
@@ -89,14 +91,19 @@ struct DecodeStepArgs {
     int b0;        // first stream of this call within `state`
 };
 
-int decode_step(const DecodeStepArgs& a, hipStream_t s) {
+// em (device copy of a kr_embed_mix): the decode kernel also runs layer 0's
+// LN1-mix of the decoded symbols for the next step; l0_mixed: the previous
+// step's decode kernel did that, so this step starts at layer 0's K, V, R
+// products.
+int decode_step(const DecodeStepArgs& a, hipStream_t s, const kr_embed_mix* em = nullptr,
+                bool l0_mixed = false) {
     KR_TRY(kr_impl_forward_layers_view(a.m, a.x, a.B, 1, a.state, a.state_B, a.b0, a.ws,
-                                       a.ws_bytes, s, a.syms));
+                                       a.ws_bytes, s, a.syms, l0_mixed));
     void* xn = kr_impl_head_scratch(a.ws, a.B, a.m->C, a.m->F);
     KR_TRY(kr_impl_head(a.m, a.x, a.B, xn, a.logits, a.ld, s, true));
-    return kr_softmax_cdf_decode(reinterpret_cast<const uint16_t*>(a.logits), a.B, a.m->V, a.ld,
-                                 a.in, a.in_len, a.base, a.limits, a.ac_states, a.syms, a.tokens,
-                                 a.tok_stride, a.tok_count, a.n_tokens, a.prec, s);
+    return kr_impl_cdf_decode(reinterpret_cast<const uint16_t*>(a.logits), a.B, a.m->V, a.ld,
+                              a.in, a.in_len, a.base, a.limits, a.ac_states, a.syms, a.tokens,
+                              a.tok_stride, a.tok_count, a.n_tokens, a.prec, em, s);
 }
 
 int check_decode(const DecodeStepArgs& a) {
@@ -220,12 +227,23 @@ int kr_decode_run(const kr_model_weights* m, int B, void* state, int32_t* syms, 
     // zero-row launch builds the plan without running a kernel.
     KR_TRY(kr_probs_to_cdf(reinterpret_cast<const float*>(logits), 0, m->V, m->V, ac_states,
                            cdf_precision, stream));
-    // One graph per step: the groups are independent branches (fork/join
-    // through events), so their latency-bound kernels overlap on the GPU.
+    // One stream group (the default): layer 0's LN1-mix of each decoded
+    // symbol runs in the decode kernel of the step that decoded it, so every
+    // step after the first starts at layer 0's K, V, R products (one launch
+    // fewer per step). Two graphs: the first step, and the later steps.
+    kr_embed_mix em_first{}, em_next{};
+    kr_embed_mix *dev_first = nullptr, *dev_next = nullptr;
+    const bool fold = ng == 1 &&
+                      kr_impl_embed_mix_args(m, B, state, B, 0, grp[0].ws, grp[0].x, true,
+                                             &em_first, &dev_first) &&
+                      kr_impl_embed_mix_args(m, B, state, B, 0, grp[0].ws, grp[0].x, false,
+                                             &em_next, &dev_next);
+    // Several groups: one graph per step, the groups as independent branches
+    // (fork/join through events), so their latency-bound kernels overlap.
     hipStream_t cap[16] = {};
     hipEvent_t ev[18] = {};
-    hipGraph_t graph = nullptr;
-    hipGraphExec_t exec = nullptr;
+    hipGraph_t graph[2] = {};
+    hipGraphExec_t exec[2] = {};
     int rc = KR_OK;
     bool capturing = false;
     auto cleanup = [&]() {
@@ -234,8 +252,8 @@ int kr_decode_run(const kr_model_weights* m, int B, void* state, int32_t* syms, 
             (void)hipStreamEndCapture(cap[0], &g2);
             if (g2) (void)hipGraphDestroy(g2);
         }
-        if (exec) (void)hipGraphExecDestroy(exec);
-        if (graph) (void)hipGraphDestroy(graph);
+        for (auto& x : exec) if (x) (void)hipGraphExecDestroy(x);
+        for (auto& g : graph) if (g) (void)hipGraphDestroy(g);
         for (auto& e : ev) if (e) (void)hipEventDestroy(e);
         for (auto& c : cap) if (c) (void)hipStreamDestroy(c);
     };
@@ -251,28 +269,46 @@ int kr_decode_run(const kr_model_weights* m, int B, void* state, int32_t* syms, 
     for (int i = 0; i < ng + 2; i++)
         if ((e = hipEventCreateWithFlags(&ev[i], hipEventDisableTiming)) != hipSuccess)
             return hip_fail(e, "event");
+    if (fold) {
+        if ((e = hipMemcpyAsync(dev_first, &em_first, sizeof em_first, hipMemcpyHostToDevice, s)) !=
+                hipSuccess ||
+            (e = hipMemcpyAsync(dev_next, &em_next, sizeof em_next, hipMemcpyHostToDevice, s)) !=
+                hipSuccess)
+            return hip_fail(e, "layer-0 mix arguments");
+    }
     // ev[0]: caller -> capture stream; ev[1]: fork; ev[2+g]: join of group g; ev[ng+1] reused at the end
     if ((e = hipEventRecord(ev[0], s)) != hipSuccess) return hip_fail(e, "record");
     if ((e = hipStreamWaitEvent(cap[0], ev[0], 0)) != hipSuccess) return hip_fail(e, "wait");
-    if ((e = hipStreamBeginCapture(cap[0], hipStreamCaptureModeThreadLocal)) != hipSuccess)
-        return hip_fail(e, "begin capture");
-    capturing = true;
-    if ((e = hipEventRecord(ev[1], cap[0])) != hipSuccess) return hip_fail(e, "fork record");
-    for (int g = 1; g < ng; g++)
-        if ((e = hipStreamWaitEvent(cap[g], ev[1], 0)) != hipSuccess) return hip_fail(e, "fork wait");
-    for (int g = 0; g < ng && rc == KR_OK; g++) rc = decode_step(grp[g], cap[g]);
-    if (rc) { cleanup(); return rc; }
-    for (int g = 1; g < ng; g++) {
-        if ((e = hipEventRecord(ev[1 + g], cap[g])) != hipSuccess) return hip_fail(e, "join record");
-        if ((e = hipStreamWaitEvent(cap[0], ev[1 + g], 0)) != hipSuccess) return hip_fail(e, "join wait");
-    }
-    e = hipStreamEndCapture(cap[0], &graph);
-    capturing = false;
-    if (e != hipSuccess) return hip_fail(e, "end capture");
-    if ((e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0)) != hipSuccess)
-        return hip_fail(e, "instantiate");
+    // graph i: step kind 0 (unfolded, or a folded run's first step) or 1 (a
+    // folded run's later steps)
+    auto capture = [&](int i) -> int {
+        hipError_t ce;
+        if ((ce = hipStreamBeginCapture(cap[0], hipStreamCaptureModeThreadLocal)) != hipSuccess)
+            return hip_fail(ce, "begin capture");
+        capturing = true;
+        if ((ce = hipEventRecord(ev[1], cap[0])) != hipSuccess) return hip_fail(ce, "fork record");
+        for (int g = 1; g < ng; g++)
+            if ((ce = hipStreamWaitEvent(cap[g], ev[1], 0)) != hipSuccess) return hip_fail(ce, "fork wait");
+        if (fold) rc = decode_step(grp[0], cap[0], i == 0 ? dev_first : dev_next, i == 1);
+        else
+            for (int g = 0; g < ng && rc == KR_OK; g++) rc = decode_step(grp[g], cap[g]);
+        if (rc) { cleanup(); return rc; }
+        for (int g = 1; g < ng; g++) {
+            if ((ce = hipEventRecord(ev[1 + g], cap[g])) != hipSuccess) return hip_fail(ce, "join record");
+            if ((ce = hipStreamWaitEvent(cap[0], ev[1 + g], 0)) != hipSuccess) return hip_fail(ce, "join wait");
+        }
+        ce = hipStreamEndCapture(cap[0], &graph[i]);
+        capturing = false;
+        if (ce != hipSuccess) return hip_fail(ce, "end capture");
+        if ((ce = hipGraphInstantiate(&exec[i], graph[i], nullptr, nullptr, 0)) != hipSuccess)
+            return hip_fail(ce, "instantiate");
+        return KR_OK;
+    };
+    if (capture(0)) return rc;
+    if (fold && n_steps > 1 && capture(1)) return rc;
     for (int i = 0; i < n_steps; i++)
-        if ((e = hipGraphLaunch(exec, cap[0])) != hipSuccess) return hip_fail(e, "graph launch");
+        if ((e = hipGraphLaunch(exec[fold && i > 0 ? 1 : 0], cap[0])) != hipSuccess)
+            return hip_fail(e, "graph launch");
     if ((e = hipEventRecord(ev[ng + 1], cap[0])) != hipSuccess) return hip_fail(e, "record");
     if ((e = hipStreamWaitEvent(s, ev[ng + 1], 0)) != hipSuccess) return hip_fail(e, "wait");
     if ((e = hipStreamSynchronize(cap[0])) != hipSuccess) return hip_fail(e, "sync");

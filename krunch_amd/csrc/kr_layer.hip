@@ -21,146 +21,10 @@
 #include "kr_gemm.h"
 #include "kr_math.h"
 #include "kr_model.h"
+#include "kr_rowops.h"
 #include "kr_wave.h"
 
 namespace {
-
-constexpr float kLnEps = 1e-5f;
-
-// ---------------------------------------------------------------------------
-// LayerNorm over one row held by one wave: lane l owns the 4-element groups
-// at columns 256*i + 4*l. Sums use a fixed lane order then an xor butterfly,
-// so every lane ends with the same value and the result is row-local.
-// ---------------------------------------------------------------------------
-template <int G>   // G = C / 256 groups of 4 per lane
-struct RowF {
-    float v[G][4];
-};
-
-template <int G>
-__device__ __forceinline__ void load_row(const kr_half* __restrict__ p, int lane, RowF<G>& r) {
-    #pragma unroll
-    for (int i = 0; i < G; i++) {
-        const kr_half4 h = *reinterpret_cast<const kr_half4*>(p + 256 * i + 4 * lane);
-        #pragma unroll
-        for (int q = 0; q < 4; q++) r.v[i][q] = (float)h[q];
-    }
-}
-
-__device__ __forceinline__ float wave_sum(float s) {
-    return kr_wave_reduce(s, [](float a, float b) { return a + b; });
-}
-
-// Per-lane copies of a [C] fp16 coefficient vector (the lane's 4-column groups).
-template <int G>
-struct CoefH {
-    kr_half4 v[G];
-};
-
-template <int G>
-__device__ __forceinline__ void load_coef(const kr_half* __restrict__ p, int lane, CoefH<G>& c) {
-    #pragma unroll
-    for (int i = 0; i < G; i++) c.v[i] = *reinterpret_cast<const kr_half4*>(p + 256 * i + 4 * lane);
-}
-
-template <int G>
-__device__ __forceinline__ void store_coef(kr_half* __restrict__ p, int lane, const CoefH<G>& c) {
-    #pragma unroll
-    for (int i = 0; i < G; i++) *reinterpret_cast<kr_half4*>(p + 256 * i + 4 * lane) = c.v[i];
-}
-
-template <int G>
-__device__ __forceinline__ void to_float(const CoefH<G>& h, RowF<G>& r) {
-    #pragma unroll
-    for (int i = 0; i < G; i++)
-        #pragma unroll
-        for (int q = 0; q < 4; q++) r.v[i][q] = (float)h.v[i][q];
-}
-
-template <int G>
-__device__ __forceinline__ void layer_norm_row(RowF<G>& r, const CoefH<G>& w, const CoefH<G>& b) {
-    constexpr float invC = 1.0f / (float)(256 * G);
-    float s = 0.0f;
-    #pragma unroll
-    for (int i = 0; i < G; i++)
-        #pragma unroll
-        for (int q = 0; q < 4; q++) s = s + r.v[i][q];
-    const float mean = wave_sum(s) * invC;
-    float ss = 0.0f;
-    #pragma unroll
-    for (int i = 0; i < G; i++)
-        #pragma unroll
-        for (int q = 0; q < 4; q++) {
-            const float d = r.v[i][q] - mean;
-            ss = ss + d * d;
-        }
-    const float rstd = 1.0f / sqrtf(wave_sum(ss) * invC + kLnEps);
-    #pragma unroll
-    for (int i = 0; i < G; i++) {
-        #pragma unroll
-        for (int q = 0; q < 4; q++) {
-            const float y = (r.v[i][q] - mean) * rstd * (float)w.v[i][q] + (float)b.v[i][q];
-            r.v[i][q] = (float)kr_f16(y);   // activations are fp16
-        }
-    }
-}
-
-template <int G>
-__device__ __forceinline__ void store_row(kr_half* __restrict__ p, int lane, const RowF<G>& r) {
-    #pragma unroll
-    for (int i = 0; i < G; i++) {
-        kr_half4 h;
-        #pragma unroll
-        for (int q = 0; q < 4; q++) h[q] = kr_f16(r.v[i][q]);
-        *reinterpret_cast<kr_half4*>(p + 256 * i + 4 * lane) = h;
-    }
-}
-
-// kr_frag_index(row, col, C) as a row part (wave-uniform: the address stays
-// in scalar registers) plus a 32-bit column part.
-__device__ __forceinline__ size_t frag_row_base(size_t row, int C) {
-    return (row >> 4) * (size_t)(C >> 5) * 512 + (row & 15) * 8;
-}
-__device__ __forceinline__ unsigned frag_col_off(int col) {
-    return (unsigned)(col >> 5) * 512u + (unsigned)((col & 31) >> 3) * 128u + (unsigned)(col & 7);
-}
-
-// Row `row` of a fragment-packed [*, C] operand (kr_frag_index): the lane's
-// 4-column groups are 4 consecutive halves there too.
-template <int G>
-__device__ __forceinline__ void store_row_frag(kr_half* __restrict__ out, size_t row, int lane,
-                                               const RowF<G>& r) {
-    constexpr int C = 256 * G;
-    #pragma unroll
-    for (int i = 0; i < G; i++) {
-        kr_half4 h;
-        #pragma unroll
-        for (int q = 0; q < 4; q++) h[q] = kr_f16(r.v[i][q]);
-        *reinterpret_cast<kr_half4*>(out + frag_row_base(row, C) + frag_col_off(256 * i + 4 * lane)) = h;
-    }
-}
-
-// mix = fp16(xx * tm + sx * (1 - tm))   (premix_kernels.cu:19-54 semantics),
-// stored into row `row` of a row-major or fragment-packed [*, C] operand.
-template <int G>
-__device__ __forceinline__ void store_mix(kr_half* __restrict__ out, size_t row, bool frag,
-                                          const CoefH<G>& tm, int lane,
-                                          const RowF<G>& cur, const RowF<G>& prev) {
-    constexpr int C = 256 * G;
-    #pragma unroll
-    for (int i = 0; i < G; i++) {
-        const kr_half4 t = tm.v[i];
-        kr_half4 h;
-        #pragma unroll
-        for (int q = 0; q < 4; q++) {
-            const float m = (float)t[q];
-            h[q] = kr_f16(cur.v[i][q] * m + prev.v[i][q] * (1.0f - m));
-        }
-        const int col = 256 * i + 4 * lane;
-        kr_half* base = out + (frag ? frag_row_base(row, C) : row * C);
-        *reinterpret_cast<kr_half4*>(base + (frag ? frag_col_off(col) : (unsigned)col)) = h;
-    }
-}
 
 // w8a8: the fp16 mix row quantised per row by the rule of kr_quantize_rows
 // (kr_gemm.h), row-major or fragment-packed for the small-M int8 GEMM. The
@@ -195,19 +59,6 @@ __device__ __forceinline__ void store_mix_q8(int8_t* __restrict__ out, float* __
     if (lane == 0) scales[row] = kr_q8_scale(amax);
 }
 
-// Weight panels to pull into each XCD's L2 while a latency-bound LN-mix runs:
-// region r holds n_groups column groups of group_bytes each (fragment-packed
-// weights, one group per workgroup column group of the product that follows);
-// the extra workgroups of XCD x read groups x, x + 8, ..., the ones that XCD's
-// workgroups will multiply by.
-struct PrefetchSet {
-    const char* base[4];
-    long long group_bytes[4];
-    int n_groups[4];
-    int n;                     // regions
-    int blocks;                // extra workgroups (a multiple of 8)
-};
-
 struct LnMixArgs {
     const kr_half* x;          // [B*T, C]
     const kr_half* ln_w;
@@ -231,54 +82,6 @@ struct LnMixArgs {
     int one_row;               // one row per workgroup (wave 0; set by the launcher)
 };
 
-// The loads only need to reach L2: their values are folded into one register
-// the compiler must keep, and nothing is stored. The 16-byte chunks XCD x
-// stages (all regions, groups x, x + 8, ...) are numbered in one sequence and
-// dealt over the XCD's staging threads, eight loads in flight per thread, so a
-// thread waits on memory about twice rather than once per group. The region
-// tables are read with constant indices only (kernel arguments in scalar
-// registers) and a chunk's region picked by selects: an array element at a
-// run-time index would be fetched from argument memory before every load,
-// and each of the eight loads would wait for the one before.
-__device__ void prefetch_panels(const PrefetchSet& pf, int p) {
-    const int x = p & 7, nr = pf.blocks >> 3;
-    const int t = (p >> 3) * 256 + (int)threadIdx.x, T = nr * 256;
-    const char* base[4];
-    long long gb[4];
-    int per[4], cum[5];
-    cum[0] = 0;
-    #pragma unroll
-    for (int i = 0; i < 4; i++) {
-        base[i] = pf.base[i];
-        gb[i] = pf.group_bytes[i];
-        const int groups_x = i < pf.n ? (pf.n_groups[i] - x + 7) / 8 : 0;   // groups x, x+8, ...
-        per[i] = i < pf.n ? (int)(gb[i] >> 4) : 1;                         // chunks per group
-        cum[i + 1] = cum[i] + groups_x * per[i];
-    }
-    unsigned acc = 0;
-    for (int c0 = t; c0 < cum[4]; c0 += 8 * T) {
-        uint4 v[8];
-        #pragma unroll
-        for (int u = 0; u < 8; u++) {
-            const int c = c0 + u * T;
-            v[u] = make_uint4(0, 0, 0, 0);
-            if (c < cum[4]) {
-                // the region holding chunk c: the last one starting at or before it
-                const bool r1 = c >= cum[1], r2 = c >= cum[2], r3 = c >= cum[3];
-                const char* b = r3 ? base[3] : (r2 ? base[2] : (r1 ? base[1] : base[0]));
-                const long long g = r3 ? gb[3] : (r2 ? gb[2] : (r1 ? gb[1] : gb[0]));
-                const int pr = r3 ? per[3] : (r2 ? per[2] : (r1 ? per[1] : per[0]));
-                const int cs = r3 ? cum[3] : (r2 ? cum[2] : (r1 ? cum[1] : cum[0]));
-                const int r = c - cs, gi = r / pr, o = r - gi * pr;
-                v[u] = reinterpret_cast<const uint4*>(b + (long long)(x + 8 * gi) * g)[o];
-            }
-        }
-        #pragma unroll
-        for (int u = 0; u < 8; u++) acc ^= v[u].x;
-    }
-    asm volatile("" :: "v"(acc));
-}
-
 // One wave per run of `run` consecutive tokens of one stream. The wave that
 // owns t = 0 reads the carried state first and rewrites it last (with the
 // LayerNorm of row T-1), so no other wave touches the state. Every
@@ -301,7 +104,7 @@ ln_mix_kernel(LnMixArgs a) {
     constexpr int C = 256 * G;
     constexpr int NM = NMIX > 0 ? NMIX : 1;
     if ((int)blockIdx.x >= a.ln_blocks) {   // staging workgroups (uniform per workgroup)
-        prefetch_panels(a.pf, (int)blockIdx.x - a.ln_blocks);
+        prefetch_panels(a.pf, (int)blockIdx.x - a.ln_blocks, (int)threadIdx.x);
         return;
     }
     const int lane = threadIdx.x & 63;
@@ -844,6 +647,12 @@ bool use_fragments(const kr_layer_weights& L, long long M) {
     return M <= KR_GEMM_SMALL_M && L.Kf && L.Vf && L.Rf && L.Of && L.fKf && L.fVf && L.fRf;
 }
 
+// Layer 0's LN1-mix can run in the previous decode kernel (kr_embed_mix)
+// when the layer is the stepped fp16 one (layer_step_fused).
+bool kr_embed_mix_layer_ok(const kr_layer_weights& L, long long M, int T) {
+    return T == 1 && !L.q8 && use_fragments(L, M);
+}
+
 // Phase marks for the layer profiler: event i is recorded on the stream
 // before phase i starts (i = 0..6) and event 7 after the last one. Phases:
 // ln1_mix, kvr_matmul, wkv, ow_matmul_residual, ln2_mix, ffn_rk_matmul,
@@ -903,11 +712,14 @@ kr_gemm_args gemm_q8_q16(const kr_half* A, int M, int K, const kr_matrix_q8& W, 
 }
 
 // Layer 0 of a forward that starts from token ids: its LN1-mix gathers the
-// embedding rows itself and writes x (no separate embed launch).
+// embedding rows itself and writes x (no separate embed launch). mixed: the
+// previous decode kernel already ran that LN1-mix (kr_embed_mix), so the
+// stepped layer starts at its K, V, R products.
 struct EmbedSrc {
     const int32_t* ids;
     const kr_half* emb;
     int V;
+    bool mixed;
 };
 
 inline void set_embed(LnMixArgs& a, const EmbedSrc* e, kr_half* x) {
@@ -1023,6 +835,20 @@ int layer_forward_q8(const kr_layer_weights& L, int C, int F, kr_half* x, int B,
     return ph.mark(7);
 }
 
+// The weights a stepped fp16 layer's LN1-mix launch stages into L2: the K, V,
+// R products' and the output projection's, as their launches deal them.
+PrefetchSet att_stage_set(const kr_layer_weights& L, int C, int M, const Work& w, kr_half* x) {
+    PrefetchSet pf{};
+    const int ns_kvr = kKvrShapes[kvr_wkv_shape(C / 256, M)][1];
+    stage_weight(pf, L.Kf, C, C, ns_kvr);
+    stage_weight(pf, L.Vf, C, C, ns_kvr);
+    stage_weight(pf, L.Rf, C, C, ns_kvr);
+    const kr_gemm_args o = gemm_args(w.ry, M, C, L.Ot, C, x, x, nullptr, L.Of, true);
+    stage_weight(pf, L.Of, C, C, kr_gemm_panel_ns(&o, 1));
+    pf.blocks = kStageBlocks;
+    return pf;
+}
+
 // Stepped (T = 1) fp16 layer with fragment-packed weights: LN1-mix, the
 // K, V, R products fused with WKV, the output projection, LN2-mix and the
 // channel mix (six launches).
@@ -1037,15 +863,9 @@ int layer_step_fused(const kr_layer_weights& L, int C, int F, kr_half* x, int B,
     // Staging bytes still cost HBM time inside the LN-mix launch; staging the
     // channel-mix R/K weights too (another 5.9 MB) lengthened LN2 by more than
     // it saved, measured on MI355X at B = 256.
-    PrefetchSet pf_att{}, pf_ffn{};
+    const PrefetchSet pf_att = att_stage_set(L, C, M, w, x);
+    PrefetchSet pf_ffn{};
     {
-        const int ns_kvr = kKvrShapes[kvr_wkv_shape(G, M)][1];
-        stage_weight(pf_att, L.Kf, C, C, ns_kvr);
-        stage_weight(pf_att, L.Vf, C, C, ns_kvr);
-        stage_weight(pf_att, L.Rf, C, C, ns_kvr);
-        const kr_gemm_args o = gemm_args(w.ry, M, C, L.Ot, C, x, x, nullptr, L.Of, true);
-        stage_weight(pf_att, L.Of, C, C, kr_gemm_panel_ns(&o, 1));
-        pf_att.blocks = kStageBlocks;
         const kr_gemm_args v = gemm_args(w.kf, M, F, L.fVt, C, x, x, w.rf, L.fVf, true);
         stage_weight(pf_ffn, L.fVf, C, F, kr_gemm_panel_ns(&v, 1));
         pf_ffn.blocks = kStageBlocks;
@@ -1064,7 +884,7 @@ int layer_step_fused(const kr_layer_weights& L, int C, int F, kr_half* x, int B,
     set_embed(a, e, x);
     a.pf = pf_att;
     KR_TRY(ph.mark(0));
-    KR_TRY(launch_ln_mix<3>(G, a, s));
+    if (!(e && e->mixed)) KR_TRY(launch_ln_mix<3>(G, a, s));
     set_embed(a, nullptr, x);
     KR_TRY(ph.mark(1));
     KvrWkvArgs kw{};
@@ -1105,6 +925,8 @@ int layer_step_fused(const kr_layer_weights& L, int C, int F, kr_half* x, int B,
 int layer_forward(const kr_layer_weights& L, int C, int F, kr_half* x, int B, int T,
                   const kr_layer_state& st, const Work& w, hipStream_t s,
                   const EmbedSrc* e = nullptr, const Phases& ph = Phases{}) {
+    KR_REQUIRE(!(e && e->mixed) || kr_embed_mix_layer_ok(L, (long long)B * T, T),
+               "forward: layer 0's LN1-mix can only be skipped in a stepped fp16 layer");
     if (L.q8) return layer_forward_q8(L, C, F, x, B, T, st, w, s, e, ph);
     const int M = B * T, G = C / 256;
     const bool fr = use_fragments(L, M);
@@ -1276,7 +1098,7 @@ int kr_impl_forward_layers(const kr_model_weights* m, void* x, int B, int T, voi
     KR_REQUIRE(B >= 1 && T >= 1 && M <= (1ll << 31) / m->F, "forward: bad B=%d T=%d", B, T);
     KR_REQUIRE(ws_bytes >= work_bytes(M, m->C, m->F), "forward: workspace too small");
     const Work w = carve(ws, M, m->C, m->F);
-    const EmbedSrc e{ids, H(m->emb), m->V};
+    const EmbedSrc e{ids, H(m->emb), m->V, false};
     for (int i = 0; i < m->n_layer; i++)
         KR_TRY(layer_forward(m->layers[i], m->C, m->F, Hm(x), B, T, state_of(state, i, B, m->C),
                              w, s, i == 0 && ids ? &e : nullptr));
@@ -1287,7 +1109,7 @@ int kr_impl_forward_layers(const kr_model_weights* m, void* x, int B, int T, voi
 // streams (one group of a larger batch; rows of each [state_B, C] component).
 int kr_impl_forward_layers_view(const kr_model_weights* m, void* x, int B, int T, void* state,
                                 int state_B, int b0, void* ws, size_t ws_bytes, hipStream_t s,
-                                const int32_t* ids) {
+                                const int32_t* ids, bool l0_mixed) {
     KR_TRY(check_model(m));
     KR_REQUIRE(x && state && ws, "forward: null pointer");
     KR_REQUIRE(b0 >= 0 && B >= 1 && b0 + B <= state_B, "forward: bad stream range");
@@ -1296,7 +1118,8 @@ int kr_impl_forward_layers_view(const kr_model_weights* m, void* x, int B, int T
     KR_REQUIRE(ws_bytes >= work_bytes(M, m->C, m->F), "forward: workspace too small");
     const Work w = carve(ws, M, m->C, m->F);
     const size_t off = (size_t)b0 * m->C;
-    const EmbedSrc e{ids, H(m->emb), m->V};
+    KR_REQUIRE(!l0_mixed || ids, "forward: a mixed layer 0 needs the token ids");
+    const EmbedSrc e{ids, H(m->emb), m->V, l0_mixed};
     for (int i = 0; i < m->n_layer; i++) {
         kr_layer_state st = state_of(state, i, state_B, m->C);
         st.att_xx = static_cast<kr_half*>(st.att_xx) + off;
@@ -1308,6 +1131,43 @@ int kr_impl_forward_layers_view(const kr_model_weights* m, void* x, int B, int T
                              i == 0 && ids ? &e : nullptr));
     }
     return KR_OK;
+}
+
+// Arguments of layer 0's LN1-mix inside the decode kernel (kr_embed_mix) for
+// a stepped forward of streams [b0, b0 + B) of a state holding state_B
+// streams, run with workspace ws and residual stream x. first: the run's
+// first step, whose carried row is the state's; later steps read the row the
+// previous step left in pend (the workspace's r rows, which the stepped fp16
+// layer does not use). *dev: where the decode kernel reads its copy of *em
+// (the workspace's k buffer, also unused there; one slot per value of first).
+// False when layer 0 is not that layer.
+bool kr_impl_embed_mix_args(const kr_model_weights* m, int B, void* state, int state_B, int b0,
+                            void* ws, void* x, bool first, kr_embed_mix* em, kr_embed_mix** dev) {
+    if (!m || !m->layers || m->n_layer < 1 || !m->emb || !state || !ws || !x || !em || !dev)
+        return false;
+    if (m->C % 256 || m->C < 256 || m->C > 1024 || B < 1 || b0 < 0 || b0 + B > state_B) return false;
+    const kr_layer_weights& L = m->layers[0];
+    if (!kr_embed_mix_layer_ok(L, B, 1)) return false;
+    const Work w = carve(ws, B, m->C, m->F);
+    kr_half* sx = static_cast<kr_half*>(state_of(state, 0, state_B, m->C).att_xx) + (size_t)b0 * m->C;
+    *em = kr_embed_mix{};
+    em->emb = H(m->emb);
+    em->V = m->V;
+    em->C = m->C;
+    em->ln_w = H(L.ln1_w);
+    em->ln_b = H(L.ln1_b);
+    em->tm[0] = H(L.tm_k); em->tm[1] = H(L.tm_v); em->tm[2] = H(L.tm_r);
+    em->out[0] = w.kx; em->out[1] = w.vx; em->out[2] = w.rx;
+    em->state = sx;
+    em->pend = w.r;
+    em->src = first ? sx : w.r;
+    em->xw = Hm(x);
+    // staged by the decode kernel's waves 4..15: 3 blocks of 256 threads per
+    // row, the rows of one XCD in whole eights
+    em->pf = att_stage_set(L, m->C, B, w, Hm(x));
+    em->pf.blocks = (B / 8) * 3 * 8;
+    *dev = reinterpret_cast<kr_embed_mix*>(w.k) + (first ? 0 : 1);
+    return true;
 }
 
 int kr_impl_embed(const kr_model_weights* m, const int32_t* ids, int M, void* x, hipStream_t s) {

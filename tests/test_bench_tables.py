@@ -16,7 +16,8 @@ def _step(tm_rk, ns_rk, ns_v):
         NS + f"gemm_panel_kernel<{tm_rk}, {ns_rk}, true, 256, false, false>(kr_gemm_multi)",
         NS + f"gemm_panel_kernel<1, {ns_v}, true, 768, false, false>(kr_gemm_multi)",
     ]
-    return layer * 12 + [
+    # layer 0's LN1-mix runs in the previous step's decode kernel
+    return layer[1:] + layer * 11 + [
         NS + "ln_mix_kernel<3, 0, false>((anonymous namespace)::LnMixArgs)",
         "_ZN12_GLOBAL__N_122gemm_head_small_kernelILi24ELi4EEEvPKDF16_S2_PDF16_xiii",
         NS + "row_cdf_kernel<0, 4>(void const*, long long, int)",
@@ -28,8 +29,8 @@ def test_step_phases_by_launch_order():
     # arguments here; only their place in the step separates them
     names = _step(1, 2, 2)
     ph = bench.step_phases(names)
-    assert ph[:6] == ["ln1", "kvr", "ow", "ln2", "rk", "fv"]
-    assert ph[6:12] == ph[:6]
+    assert ph[:11] == ["kvr", "ow", "ln2", "rk", "fv", "ln1", "kvr", "ow", "ln2", "rk", "fv"]
+    assert ph[11:17] == ph[5:11]
     assert ph[-3:] == ["lnout", "head", "cdf"]
     keys = [k for k, *_ in bench.step_kernel_bytes(128)]
     assert set(ph) == set(keys)

@@ -160,3 +160,61 @@ def test_blob_header_roundtrip():
     assert len(h) == HEADER_SIZE == 37
     d = decode_header(h)
     assert (d["original_len"], d["n_chunks"], d["crc32"], d["model_id"]) == (123456, 7, 0xDEADBEEF, 1)
+
+
+def _decode_direct(eng, enc, splits, use_graph):
+    """kr_decode_run over `enc` in len(splits) calls of splits[i] steps each;
+    returns every buffer the calls leave behind (tokens, counts, coder and
+    model state, next symbols)."""
+    from krunch_amd import _lib
+    from krunch_amd.inference import CDF_PRECISION
+    from krunch_amd.model import State
+    P = eng.weights["prepared"]
+    dev = P.device
+    B = len(enc)
+    n_tok = [struct.unpack(">II", e[:8])[1] for e in enc]
+    streams = [e[8:] for e in enc]
+    offs = np.cumsum([0] + [len(s) for s in streams])
+    inbuf = torch.from_numpy(np.frombuffer(b"".join(streams) + b"\0", dtype=np.uint8).copy()).to(dev)
+    base = torch.from_numpy(offs[:-1].astype(np.int32)).to(dev)
+    limits = torch.tensor([len(s) for s in streams], dtype=torch.int32, device=dev)
+    ac = torch.empty((B, 4), dtype=torch.uint32, device=dev)
+    s = _lib.stream_ptr()
+    _lib.call("kr_decode_init_batched", inbuf.data_ptr(), inbuf.numel(), base.data_ptr(),
+              limits.data_ptr(), ac.data_ptr(), B, s)
+    Tmax = max(n_tok)
+    state = State(P.n_layer, B, P.C, dev)
+    syms = torch.zeros(B, dtype=torch.int32, device=dev)
+    tokens = torch.zeros((B, Tmax), dtype=torch.int32, device=dev)
+    count = torch.zeros(B, dtype=torch.int32, device=dev)
+    ntd = torch.tensor(n_tok, dtype=torch.int32, device=dev)
+    x = torch.empty((B, P.C), dtype=torch.float16, device=dev)
+    nbytes = _lib.lib().kr_decode_workspace_bytes(B, 1, P.C, P.F)
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+    ld = cpp_path.logits_ld(P.V)
+    logits = torch.empty((B, ld), dtype=torch.float16, device=dev)
+    for n in splits:
+        _lib.call("kr_decode_run", P.ptr, B, state.ptr, syms.data_ptr(), x.data_ptr(),
+                  ws.data_ptr(), nbytes, logits.data_ptr(), ld, inbuf.data_ptr(), inbuf.numel(),
+                  base.data_ptr(), limits.data_ptr(), ac.data_ptr(), tokens.data_ptr(), Tmax,
+                  count.data_ptr(), ntd.data_ptr(), CDF_PRECISION, n, 1, 1 if use_graph else 0, s)
+    torch.cuda.synchronize()
+    return [t.cpu() for t in (tokens, count, ac, syms, state.buf)]
+
+
+def test_graph_decode_leaves_the_eager_state(eng):
+    """The graph decode runs layer 0's LN1-mix of each decoded symbol inside
+    that step's decode kernel and carries layer 0's shifted row one step
+    late. Split over calls of any length, it leaves the model state, coder
+    state and tokens byte-equal to the eager decode (which runs every layer's
+    own LN1-mix), also for streams that finished before the last step."""
+    lens = [40, 17, 33, 5, 1]
+    toks = [synthetic.zipf_tokens(1, n, seed_base=3100 + i)[0] for i, n in enumerate(lens)]
+    enc = eng.compress_tokens_batched(toks)
+    ref = _decode_direct(eng, enc, [45], use_graph=False)
+    for b, t in enumerate(toks):
+        np.testing.assert_array_equal(ref[0][b, :len(t)].numpy(), t)
+    for splits in ([45], [20, 25], [1, 1, 43], [17, 3, 25]):
+        got = _decode_direct(eng, enc, splits, use_graph=True)
+        for name, a, g in zip(("tokens", "count", "coder", "syms", "model state"), ref, got):
+            assert torch.equal(a, g), f"{name} differs after calls of {splits} steps"
