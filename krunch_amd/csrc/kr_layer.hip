@@ -26,39 +26,6 @@
 
 namespace {
 
-// w8a8: the fp16 mix row quantised per row by the rule of kr_quantize_rows
-// (kr_gemm.h), row-major or fragment-packed for the small-M int8 GEMM. The
-// mixes are held as fp16 while the row maximum is reduced (half the
-// registers of fp32 copies; LN-mix occupancy matters, see ln_mix_kernel).
-template <int G>
-__device__ __forceinline__ void store_mix_q8(int8_t* __restrict__ out, float* __restrict__ scales,
-                                             size_t row, bool frag, const CoefH<G>& tm, int lane,
-                                             const RowF<G>& cur, const RowF<G>& prev) {
-    constexpr int C = 256 * G;
-    kr_half4 h[G];
-    float amax = 0.0f;
-    #pragma unroll
-    for (int i = 0; i < G; i++)
-        #pragma unroll
-        for (int q = 0; q < 4; q++) {
-            const float m = (float)tm.v[i][q];
-            h[i][q] = kr_f16(cur.v[i][q] * m + prev.v[i][q] * (1.0f - m));
-            amax = fmaxf(amax, fabsf((float)h[i][q]));
-        }
-    amax = kr_wave_reduce(amax, [](float a, float b) { return fmaxf(a, b); });
-    const float inv = kr_q8_inv(amax);
-    #pragma unroll
-    for (int i = 0; i < G; i++) {
-        const uint32_t w = kr_q8_pack4((float)h[i][0], (float)h[i][1], (float)h[i][2],
-                                       (float)h[i][3], inv);
-        const int col = 256 * i + 4 * lane;
-        // kr_frag_index_i8 (col even): twice the 16-bit view's index
-        int8_t* base = out + (frag ? 2 * frag_row_base(row, C / 2) : row * C);
-        *reinterpret_cast<uint32_t*>(base + (frag ? 2 * frag_col_off(col / 2) : (unsigned)col)) = w;
-    }
-    if (lane == 0) scales[row] = kr_q8_scale(amax);
-}
-
 struct LnMixArgs {
     const kr_half* x;          // [B*T, C]
     const kr_half* ln_w;
@@ -647,10 +614,17 @@ bool use_fragments(const kr_layer_weights& L, long long M) {
     return M <= KR_GEMM_SMALL_M && L.Kf && L.Vf && L.Rf && L.Of && L.fKf && L.fVf && L.fRf;
 }
 
+// The int8 layer's small-M fragment path (its weights fragment-packed).
+bool use_fragments_q8(const kr_layer_q8& Q, long long M) {
+    return M <= KR_GEMM_SMALL_M && Q.K.qf && Q.V.qf && Q.R.qf && Q.O.qf && Q.fK.qf && Q.fV.qf &&
+           Q.fR.qf;
+}
+
 // Layer 0's LN1-mix can run in the previous decode kernel (kr_embed_mix)
-// when the layer is the stepped fp16 one (layer_step_fused).
+// when the layer is a stepped one on fragment-packed weights
+// (layer_step_fused, or layer_forward_q8's stepped path).
 bool kr_embed_mix_layer_ok(const kr_layer_weights& L, long long M, int T) {
-    return T == 1 && !L.q8 && use_fragments(L, M);
+    return T == 1 && (L.q8 ? use_fragments_q8(*L.q8, M) : use_fragments(L, M));
 }
 
 // Phase marks for the layer profiler: event i is recorded on the stream
@@ -729,13 +703,36 @@ inline void set_embed(LnMixArgs& a, const EmbedSrc* e, kr_half* x) {
     a.xw = e ? x : nullptr;
 }
 
+// The weights a stepped layer's LN1-mix launch stages into L2: the K, V, R
+// products' and the output projection's (fp16 or int8), as their launches
+// deal them.
+PrefetchSet att_stage_set(const kr_layer_weights& L, int C, int M, const Work& w, kr_half* x) {
+    PrefetchSet pf{};
+    const int ns_kvr = kKvrShapes[kvr_wkv_shape(C / 256, M)][1];
+    if (L.q8) {
+        const kr_layer_q8& Q = *L.q8;
+        stage_weight(pf, Q.K.qf, C, C, ns_kvr, 1);
+        stage_weight(pf, Q.V.qf, C, C, ns_kvr, 1);
+        stage_weight(pf, Q.R.qf, C, C, ns_kvr, 1);
+        const kr_gemm_args o = gemm_q8_q16(w.ry, M, C, Q.O, C, x, x);
+        stage_weight(pf, Q.O.qf, C, C, kr_gemm_panel_ns(&o, 1), 1);
+    } else {
+        stage_weight(pf, L.Kf, C, C, ns_kvr);
+        stage_weight(pf, L.Vf, C, C, ns_kvr);
+        stage_weight(pf, L.Rf, C, C, ns_kvr);
+        const kr_gemm_args o = gemm_args(w.ry, M, C, L.Ot, C, x, x, nullptr, L.Of, true);
+        stage_weight(pf, L.Of, C, C, kr_gemm_panel_ns(&o, 1));
+    }
+    pf.blocks = kStageBlocks;
+    return pf;
+}
+
 int layer_forward_q8(const kr_layer_weights& L, int C, int F, kr_half* x, int B, int T,
                      const kr_layer_state& st, const Work& w, hipStream_t s,
                      const EmbedSrc* e, const Phases& ph) {
     const kr_layer_q8& Q = *L.q8;
     const int M = B * T, G = C / 256;
-    const bool fr = M <= KR_GEMM_SMALL_M && Q.K.qf && Q.V.qf && Q.R.qf && Q.O.qf && Q.fK.qf &&
-                    Q.fV.qf && Q.fR.qf;
+    const bool fr = use_fragments_q8(Q, M);
     LnMixArgs a{};
     a.x = x;
     a.ln_w = H(L.ln1_w);
@@ -753,19 +750,13 @@ int layer_forward_q8(const kr_layer_weights& L, int C, int F, kr_half* x, int B,
     // their XCDs' L2, LN2 the value product's (as layer_step_fused does)
     PrefetchSet pf_ffn{};
     if (fr && T == 1) {
-        const int ns_kvr = kKvrShapes[kvr_wkv_shape(G, M)][1];
-        stage_weight(a.pf, Q.K.qf, C, C, ns_kvr, 1);
-        stage_weight(a.pf, Q.V.qf, C, C, ns_kvr, 1);
-        stage_weight(a.pf, Q.R.qf, C, C, ns_kvr, 1);
-        const kr_gemm_args o = gemm_q8_q16(w.ry, M, C, Q.O, C, x, x);
-        stage_weight(a.pf, Q.O.qf, C, C, kr_gemm_panel_ns(&o, 1), 1);
-        a.pf.blocks = kStageBlocks;
+        a.pf = att_stage_set(L, C, M, w, x);
         const kr_gemm_args v = gemm_q8_q16(w.kf, M, F, Q.fV, C, x, x, w.rf);
         stage_weight(pf_ffn, Q.fV.qf, C, F, kr_gemm_panel_ns(&v, 1), 1);
         pf_ffn.blocks = kStageBlocks;
     }
     KR_TRY(ph.mark(0));
-    KR_TRY(launch_ln_mix<3>(G, a, s));
+    if (!(e && e->mixed)) KR_TRY(launch_ln_mix<3>(G, a, s));
     set_embed(a, nullptr, x);
     a.pf = pf_ffn;
     KR_TRY(ph.mark(1));
@@ -833,20 +824,6 @@ int layer_forward_q8(const kr_layer_weights& L, int C, int F, kr_half* x, int B,
                               KR_EP_GATED, s));
     }
     return ph.mark(7);
-}
-
-// The weights a stepped fp16 layer's LN1-mix launch stages into L2: the K, V,
-// R products' and the output projection's, as their launches deal them.
-PrefetchSet att_stage_set(const kr_layer_weights& L, int C, int M, const Work& w, kr_half* x) {
-    PrefetchSet pf{};
-    const int ns_kvr = kKvrShapes[kvr_wkv_shape(C / 256, M)][1];
-    stage_weight(pf, L.Kf, C, C, ns_kvr);
-    stage_weight(pf, L.Vf, C, C, ns_kvr);
-    stage_weight(pf, L.Rf, C, C, ns_kvr);
-    const kr_gemm_args o = gemm_args(w.ry, M, C, L.Ot, C, x, x, nullptr, L.Of, true);
-    stage_weight(pf, L.Of, C, C, kr_gemm_panel_ns(&o, 1));
-    pf.blocks = kStageBlocks;
-    return pf;
 }
 
 // Stepped (T = 1) fp16 layer with fragment-packed weights: LN1-mix, the
@@ -1158,6 +1135,10 @@ bool kr_impl_embed_mix_args(const kr_model_weights* m, int B, void* state, int s
     em->ln_b = H(L.ln1_b);
     em->tm[0] = H(L.tm_k); em->tm[1] = H(L.tm_v); em->tm[2] = H(L.tm_r);
     em->out[0] = w.kx; em->out[1] = w.vx; em->out[2] = w.rx;
+    if (L.q8) {
+        em->q[0] = w.kx8; em->q[1] = w.vx8; em->q[2] = w.rx8;
+        em->qs[0] = w.kxs; em->qs[1] = w.vxs; em->qs[2] = w.rxs;
+    }
     em->state = sx;
     em->pend = w.r;
     em->src = first ? sx : w.r;

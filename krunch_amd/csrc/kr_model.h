@@ -31,7 +31,8 @@ struct PrefetchSet {
 // starts at layer 0's K, V, R products. Row b of the next step:
 //   xw[b]  = emb[id]                                  (the residual stream)
 //   xx     = LN1(emb[id]);  sx = src[b]               (the carried row)
-//   out[m] = mix(xx, sx) with tm[m], fragment-packed  (K, V, R operands)
+//   out[m] = mix(xx, sx) with tm[m], fragment-packed  (K, V, R operands;
+//            w8a8: q[m], qs[m], quantised per row)
 //   state[b] = sx;  pend[b] = xx
 // The carried row is committed one step late: after a step, state holds the
 // row of the token that step consumed (what the layer's own LN1-mix would
@@ -46,6 +47,8 @@ struct kr_embed_mix {
     const kr_half* ln_b;
     const kr_half* tm[3];
     kr_half* out[3];
+    int8_t* q[3];              // w8a8 layer 0 (q[0] non-null): int8 mixes instead of out[]
+    float* qs[3];              // and their row scales (kr_quantize_rows rule)
     const kr_half* src;        // [B, C]
     kr_half* state;            // [B, C] layer 0's att_xx
     kr_half* pend;             // [B, C]

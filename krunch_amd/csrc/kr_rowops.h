@@ -5,6 +5,7 @@
 // any kernel that runs it.
 #pragma once
 #include "kr_common.h"
+#include "kr_gemm.h"
 #include "kr_model.h"
 #include "kr_wave.h"
 
@@ -147,6 +148,39 @@ __device__ __forceinline__ void store_mix(kr_half* __restrict__ out, size_t row,
     }
 }
 
+// w8a8: the fp16 mix row quantised per row by the rule of kr_quantize_rows
+// (kr_gemm.h), row-major or fragment-packed for the small-M int8 GEMM. The
+// mixes are held as fp16 while the row maximum is reduced (half the
+// registers of fp32 copies; LN-mix occupancy matters, see ln_mix_kernel).
+template <int G>
+__device__ __forceinline__ void store_mix_q8(int8_t* __restrict__ out, float* __restrict__ scales,
+                                             size_t row, bool frag, const CoefH<G>& tm, int lane,
+                                             const RowF<G>& cur, const RowF<G>& prev) {
+    constexpr int C = 256 * G;
+    kr_half4 h[G];
+    float amax = 0.0f;
+    #pragma unroll
+    for (int i = 0; i < G; i++)
+        #pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const float m = (float)tm.v[i][q];
+            h[i][q] = kr_f16(cur.v[i][q] * m + prev.v[i][q] * (1.0f - m));
+            amax = fmaxf(amax, fabsf((float)h[i][q]));
+        }
+    amax = kr_wave_reduce(amax, [](float a, float b) { return fmaxf(a, b); });
+    const float inv = kr_q8_inv(amax);
+    #pragma unroll
+    for (int i = 0; i < G; i++) {
+        const uint32_t w = kr_q8_pack4((float)h[i][0], (float)h[i][1], (float)h[i][2],
+                                       (float)h[i][3], inv);
+        const int col = 256 * i + 4 * lane;
+        // kr_frag_index_i8 (col even): twice the 16-bit view's index
+        int8_t* base = out + (frag ? 2 * frag_row_base(row, C / 2) : row * C);
+        *reinterpret_cast<uint32_t*>(base + (frag ? 2 * frag_col_off(col / 2) : (unsigned)col)) = w;
+    }
+    if (lane == 0) scales[row] = kr_q8_scale(amax);
+}
+
 // The loads only need to reach L2: their values are folded into one register
 // the compiler must keep, and nothing is stored. The 16-byte chunks XCD x
 // stages (all regions, groups x, x + 8, ...) are numbered in one sequence and
@@ -215,7 +249,10 @@ __device__ __forceinline__ void embed_mix_row(const kr_embed_mix& e, size_t b, i
     to_float<G>(cur_h, cur);
     layer_norm_row<G>(cur, w, bias);
     #pragma unroll
-    for (int m = 0; m < 3; m++) store_mix<G>(e.out[m], b, true, tm[m], lane, cur, prev);
+    for (int m = 0; m < 3; m++) {
+        if (e.q[0]) store_mix_q8<G>(e.q[m], e.qs[m], b, true, tm[m], lane, cur, prev);
+        else store_mix<G>(e.out[m], b, true, tm[m], lane, cur, prev);
+    }
     store_row<G>(e.pend + b * C, lane, cur);
 }
 

@@ -202,12 +202,22 @@ def _decode_direct(eng, enc, splits, use_graph):
     return [t.cpu() for t in (tokens, count, ac, syms, state.buf)]
 
 
-def test_graph_decode_leaves_the_eager_state(eng):
+@pytest.fixture(scope="module")
+def eng_w8a8():
+    e = InferenceEngine()
+    e.window = 64
+    return e.load(synthetic.make_weights(), w8a8=True)
+
+
+@pytest.mark.parametrize("codec", ["fp16", "w8a8"])
+def test_graph_decode_leaves_the_eager_state(eng, eng_w8a8, codec):
     """The graph decode runs layer 0's LN1-mix of each decoded symbol inside
     that step's decode kernel and carries layer 0's shifted row one step
     late. Split over calls of any length, it leaves the model state, coder
     state and tokens byte-equal to the eager decode (which runs every layer's
-    own LN1-mix), also for streams that finished before the last step."""
+    own LN1-mix), also for streams that finished before the last step. The
+    w8a8 codec's layer 0 writes its mixes quantised per row there."""
+    eng = eng_w8a8 if codec == "w8a8" else eng
     lens = [40, 17, 33, 5, 1]
     toks = [synthetic.zipf_tokens(1, n, seed_base=3100 + i)[0] for i, n in enumerate(lens)]
     enc = eng.compress_tokens_batched(toks)
