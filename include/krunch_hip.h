@@ -350,7 +350,11 @@ int kr_decode_step(const kr_model_weights* m, int B, void* state, int32_t* syms,
  * kr_decode_workspace_bytes); with use_graph one step is captured into a HIP
  * graph whose groups are parallel branches, so their latency-bound kernels
  * overlap, and the graph is replayed n_steps times (the reference's graph
- * path, cpp_path.py:229-276). Synchronous with respect to the work it enqueues. */
+ * path, cpp_path.py:229-276). With one group, the graph's decode kernel also
+ * runs layer 0's LN1-mix of each decoded symbol for the next step (a first-
+ * step graph and a later-steps graph); the state, tokens and coder state it
+ * leaves are those of the eager path (use_graph = 0), x and ws are scratch.
+ * Synchronous with respect to the work it enqueues. */
 size_t kr_decode_workspace_bytes(int B, int n_groups, int C, int F);
 int kr_decode_run(const kr_model_weights* m, int B, void* state, int32_t* syms, void* x,
                   void* ws, size_t ws_bytes, void* logits, long long ld,
