@@ -292,20 +292,35 @@ __device__ __forceinline__ void store_row4(const kr_gemm_args& g, int m, int n, 
     }
 }
 
-// Tile t of the launch (same dealing as tile_of, for a launch of `grid`
-// virtual blocks): false past the last tile.
-__device__ __forceinline__ bool big_tile(const kr_gemm_args& g, int vb, int& m_t, int& n_t) {
+// Tile t of the launch (the dealing of tile_of, for a launch of `grid`
+// virtual blocks, in groups of group_m row tiles): false past the last tile.
+__device__ __forceinline__ bool big_tile(const kr_gemm_args& g, int vb, int group_m, int& m_t,
+                                         int& n_t) {
     const int gy = (g.M + kBigM - 1) / kBigM, gx = (g.N + kBigN - 1) / kBigN;
     const int T = gx * gy, per = (T + 7) / 8;
     const int t = (vb & 7) * per + (vb >> 3);
     if (t >= T || (vb >> 3) >= per) return false;
-    const int in_group = kGroupM * gx;
-    const int first_m = (t / in_group) * kGroupM;
-    const int gm = min(gy - first_m, kGroupM);
+    const int in_group = group_m * gx;
+    const int first_m = (t / in_group) * group_m;
+    const int gm = min(gy - first_m, group_m);
     const int r = t % in_group;
     m_t = first_m + r % gm;
     n_t = r / gm;
     return true;
+}
+
+// Row tiles per group of the persistent kernel's tile order: as many as keep
+// an XCD's A panels (group_m x 256 rows x K) within about half of its 4 MB
+// L2, at most 8 (fp16: 5 at K = 768, 1 at K = 3072). Measured on MI355X:
+// the head at K = 768 runs 439 -> 395 us per 4096-row launch with 5 row
+// tiles per group instead of 8 (8 put 3 MB of A panels in each L2), and
+// the channel-mix value product at K = 3072 is fastest with 1; the fp16
+// compress window takes 118.5-118.9 ms against 120.1-120.7 at 8 (A B A B
+// on one box, same bits), w8a8 compress +1.1%.
+int big_group_m(int K, bool i8) {
+    const long long panel = (long long)kBigM * K * (i8 ? 1 : 2);
+    const long long g = (2ll << 20) / panel;
+    return (int)std::min<long long>(8, std::max<long long>(1, g));
 }
 
 // Persistent: workgroup w takes virtual blocks w, w + G, w + 2G, ... (G =
@@ -316,7 +331,7 @@ __device__ __forceinline__ bool big_tile(const kr_gemm_args& g, int vb, int& m_t
 // int8 k and each 32-half block one v_mfma_i32_16x16x64_i8; the int32 sum is
 // exact (no slices), dequantised once per output: (float(acc) * sa[m]) * sw[n].
 template <int EP, bool I8>
-__global__ void __launch_bounds__(512, 1) gemm_big_kernel(kr_gemm_args g, int n_virtual) {
+__global__ void __launch_bounds__(512, 1) gemm_big_kernel(kr_gemm_args g, int n_virtual, int group_m) {
     __shared__ __attribute__((aligned(1024))) kr_half8 ring[3 * kBigStage];   // 3 x 48 KB
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -356,7 +371,7 @@ __global__ void __launch_bounds__(512, 1) gemm_big_kernel(kr_gemm_args g, int n_
     };
 
     int vb = blockIdx.x, m_t, n_t;
-    if (!big_tile(g, vb, m_t, n_t)) return;
+    if (!big_tile(g, vb, group_m, m_t, n_t)) return;
     const char* src[6];
     const char* nsrc[6];
     sources(m_t * kBigM, n_t * kBigN, src);
@@ -371,7 +386,7 @@ __global__ void __launch_bounds__(512, 1) gemm_big_kernel(kr_gemm_args g, int n_
     while (true) {
         const int m0 = m_t * kBigM, n0 = n_t * kBigN;
         int nm_t = 0, nn_t = 0;
-        const bool has_next = vb + G < n_virtual && big_tile(g, vb + G, nm_t, nn_t);
+        const bool has_next = vb + G < n_virtual && big_tile(g, vb + G, group_m, nm_t, nn_t);
         if (has_next) sources(nm_t * kBigM, nn_t * kBigN, nsrc);
         typedef typename std::conditional<I8, kr_int4, kr_float4>::type Acc;
         Acc acc[4][4];
@@ -468,13 +483,14 @@ int launch_big(const kr_gemm_args& g, int ep, hipStream_t s) {
     const long long T = (long long)((g.N + kBigN - 1) / kBigN) * ((g.M + kBigM - 1) / kBigM);
     const int n_virtual = (int)((T + 7) / 8 * 8);
     const int grid = n_virtual < 256 ? n_virtual : 256;   // one workgroup per CU
+    const int gm = big_group_m(g.K, I8);
     switch (ep) {
-        case KR_EP_F32: gemm_big_kernel<KR_EP_F32, I8><<<grid, 512, 0, s>>>(g, n_virtual); break;
-        case KR_EP_F16: gemm_big_kernel<KR_EP_F16, I8><<<grid, 512, 0, s>>>(g, n_virtual); break;
-        case KR_EP_SIGMOID: gemm_big_kernel<KR_EP_SIGMOID, I8><<<grid, 512, 0, s>>>(g, n_virtual); break;
-        case KR_EP_RELUSQ: gemm_big_kernel<KR_EP_RELUSQ, I8><<<grid, 512, 0, s>>>(g, n_virtual); break;
-        case KR_EP_RESID: gemm_big_kernel<KR_EP_RESID, I8><<<grid, 512, 0, s>>>(g, n_virtual); break;
-        case KR_EP_GATED: gemm_big_kernel<KR_EP_GATED, I8><<<grid, 512, 0, s>>>(g, n_virtual); break;
+        case KR_EP_F32: gemm_big_kernel<KR_EP_F32, I8><<<grid, 512, 0, s>>>(g, n_virtual, gm); break;
+        case KR_EP_F16: gemm_big_kernel<KR_EP_F16, I8><<<grid, 512, 0, s>>>(g, n_virtual, gm); break;
+        case KR_EP_SIGMOID: gemm_big_kernel<KR_EP_SIGMOID, I8><<<grid, 512, 0, s>>>(g, n_virtual, gm); break;
+        case KR_EP_RELUSQ: gemm_big_kernel<KR_EP_RELUSQ, I8><<<grid, 512, 0, s>>>(g, n_virtual, gm); break;
+        case KR_EP_RESID: gemm_big_kernel<KR_EP_RESID, I8><<<grid, 512, 0, s>>>(g, n_virtual, gm); break;
+        case KR_EP_GATED: gemm_big_kernel<KR_EP_GATED, I8><<<grid, 512, 0, s>>>(g, n_virtual, gm); break;
         default: return kr_fail(KR_EINVAL, "unknown epilogue %d", ep);
     }
     KR_LAUNCHED();
