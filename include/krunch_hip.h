@@ -207,8 +207,10 @@ int kr_quantize_rows(const uint16_t* x, long long ldx, int M, int K, int8_t* q, 
  * view, K/2 columns), M <= 512; packed = 0: both row-major [*, K];
  * packed = 2: as 1, but xq points to fp16 activations, fragment-packed
  * (kr_pack_fragments layout), which the product quantises per row on load
- * by the rule above (sa is not read and may be null) - the same bits as
- * kr_quantize_rows followed by packed = 1, in one launch. */
+ * by the rule above (sa is not read and may be null) - for finite
+ * activations, the same bits as kr_quantize_rows followed by packed = 1, in
+ * one launch (the row maximum compares fp16 bit patterns, so a NaN in a row
+ * gives that row a NaN scale, where kr_quantize_rows' fmaxf skips it). */
 int kr_det_matmul_i8(const int8_t* xq, const float* sa, int M, int K, const int8_t* wq,
                      const float* sw, int N, void* out, long long ldo, int epilogue,
                      const uint16_t* res, const uint16_t* gate, int packed, void* stream);

@@ -15,6 +15,7 @@ Additions: `forward_packed_batched` runs B chunks x T tokens in one call
 from __future__ import annotations
 
 import os
+from collections import OrderedDict
 
 import torch
 
@@ -23,7 +24,12 @@ from krunch_amd.model import Prepared, State, prepare
 
 N_LAYER = 12
 CDF_PRECISION = 24
-_WEIGHTS_CACHE: dict = {}
+# Prepared bundles by (id(model), device, codec), least recently used first.
+# Each entry holds the model itself, so its id cannot be reused while the
+# entry lives; at most WEIGHTS_CACHE_SIZE entries are kept (one prepared
+# 169M-shape fp16 model is ~350 MB of device memory).
+WEIGHTS_CACHE_SIZE = 4
+_WEIGHTS_CACHE: "OrderedDict" = OrderedDict()
 
 
 class Workspace:
@@ -61,14 +67,27 @@ def init_weights(model, device: str = "cuda", w8a8: bool = False) -> dict:
     (rwkv-package keys, [in,out] matrices, raw time_decay) or is such a dict.
     w8a8=True selects the int8 codec (head stays fp16)."""
     key = (id(model), str(device), bool(w8a8))
-    if key in _WEIGHTS_CACHE:
-        return _WEIGHTS_CACHE[key]
+    hit = _WEIGHTS_CACHE.get(key)
+    if hit is not None and hit["model"] is model:
+        _WEIGHTS_CACHE.move_to_end(key)
+        return hit
     w = model.w if hasattr(model, "w") else model
     P = prepare(w, device, w8a8=w8a8)
     bundle = {"prepared": P, "n_embd": P.C, "n_att": P.C, "n_ffn": P.F, "n_vocab": P.V,
               "n_layer": P.n_layer, "device": P.device, "model": model}
     _WEIGHTS_CACHE[key] = bundle
+    while len(_WEIGHTS_CACHE) > WEIGHTS_CACHE_SIZE:
+        _WEIGHTS_CACHE.popitem(last=False)
     return bundle
+
+
+def release_weights(model=None):
+    """Drop the prepared copies of `model` (every device and codec), or of
+    every model when None. Bundles a caller still holds stay valid."""
+    for key in [k for k, v in _WEIGHTS_CACHE.items() if model is None or v["model"] is model]:
+        del _WEIGHTS_CACHE[key]
+        for gk in [g for g, hit in _STEP_GRAPHS.items() if hit[-1]["model"] is model or model is None]:
+            del _STEP_GRAPHS[gk]
 
 
 def fresh_state(weights: dict) -> State:
@@ -165,9 +184,11 @@ def forward_stepped_graphed(weights: dict, last_token: int, state: State) -> tor
                       nbytes, s)
             _lib.call("kr_head_logits", P.ptr, x.data_ptr(), 1, xn.data_ptr(), logits.data_ptr(),
                       P.V, s)
-        hit = (graph, ids, x, xn, logits, ws)
+        # the entry holds the weights bundle, so its id cannot be reused for
+        # another bundle while the graph (which points into it) is cached
+        hit = (graph, ids, x, xn, logits, ws, weights)
         _STEP_GRAPHS[key] = hit
-    graph, ids, _, _, logits, _ = hit
+    graph, ids, _, _, logits, _, _ = hit
     tok = int(last_token)
     if not 0 <= tok < P.V:
         raise ValueError(f"token id out of range [0, {P.V})")

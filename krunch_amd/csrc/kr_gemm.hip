@@ -531,9 +531,11 @@ int launch_big(const kr_gemm_args& g, int ep, hipStream_t s) {
 // QA (w8a8, a_q16): A arrives as fp16 in the fp16 fragment layout and is
 // quantised here, one scale per row: each wave takes max |x| over its slice
 // of its rows, the waves meet in LDS for the row maximum, and every wave
-// rounds its own slice to int8 (kr_q8_pack4) in registers. The bits are those
-// of kr_quantize_rows followed by the int8 product, without the separate
-// quantisation launch; the cost is twice the A bytes.
+// rounds its own slice to int8 (kr_q8_pack4) in registers. For finite
+// activations the bits are those of kr_quantize_rows followed by the int8
+// product, without the separate quantisation launch; the cost is twice the A
+// bytes. (The maximum compares fp16 bit patterns, so a NaN outranks every
+// finite value here, where kr_quantize_rows' fmaxf skips it.)
 constexpr int kEpiPrefetch = 4;   // epilogue tiles per wave with prefetched res/gate
 
 typedef unsigned short kr_u16x2 __attribute__((ext_vector_type(2)));

@@ -903,7 +903,8 @@ int layer_forward(const kr_layer_weights& L, int C, int F, kr_half* x, int B, in
                   const kr_layer_state& st, const Work& w, hipStream_t s,
                   const EmbedSrc* e = nullptr, const Phases& ph = Phases{}) {
     KR_REQUIRE(!(e && e->mixed) || kr_embed_mix_layer_ok(L, (long long)B * T, T),
-               "forward: layer 0's LN1-mix can only be skipped in a stepped fp16 layer");
+               "forward: layer 0's LN1-mix can only be skipped in a stepped layer on "
+               "fragment-packed weights (fp16 or w8a8)");
     if (L.q8) return layer_forward_q8(L, C, F, x, B, T, st, w, s, e, ph);
     const int M = B * T, G = C / 256;
     const bool fr = use_fragments(L, M);
@@ -1123,8 +1124,12 @@ bool kr_impl_embed_mix_args(const kr_model_weights* m, int B, void* state, int s
     if (!m || !m->layers || m->n_layer < 1 || !m->emb || !state || !ws || !x || !em || !dev)
         return false;
     if (m->C % 256 || m->C < 256 || m->C > 1024 || B < 1 || b0 < 0 || b0 + B > state_B) return false;
+    // every layer must be a stepped layer on fragment-packed weights: only
+    // those leave the workspace's r rows (pend) and k buffer (the
+    // descriptors) alone between two decode kernels
+    for (int i = 0; i < m->n_layer; i++)
+        if (!kr_embed_mix_layer_ok(m->layers[i], B, 1)) return false;
     const kr_layer_weights& L = m->layers[0];
-    if (!kr_embed_mix_layer_ok(L, B, 1)) return false;
     const Work w = carve(ws, B, m->C, m->F);
     kr_half* sx = static_cast<kr_half*>(state_of(state, 0, state_B, m->C).att_xx) + (size_t)b0 * m->C;
     *em = kr_embed_mix{};

@@ -295,14 +295,16 @@ def rwkv4_layer_step_cpp_graphed(layer_id, x_buf, x_out_buf, att_xx, aa, bb, pp,
     executes nothing here, so every call - the first included - advances the
     state exactly once; the reference's warm-up runs and capture advance it
     three times on the first call (cpp_path.py:369-384 records that as a bug).
-    The graph also keys on the buffer addresses, so new buffers get a new graph
-    instead of a stale replay."""
+    The graph also keys on the buffer addresses and shapes, so new buffers get
+    a new graph instead of a stale replay. The graph runs on the transposed
+    weight copies made at capture time: after an in-place change of a
+    weight tensor (same address), call clear_layer_graph_cache()."""
     _cuda(x_buf, torch.float16, "x_buf")
     _cuda(x_out_buf, torch.float16, "x_out_buf")
     _check(x_buf.shape == x_out_buf.shape, "x_buf and x_out_buf must have the same shape")
-    key = (int(layer_id), int(x_buf.shape[1]), x_buf.data_ptr(), x_out_buf.data_ptr(),
-           att_xx.data_ptr(), aa.data_ptr(), bb.data_ptr(), pp.data_ptr(), ffn_xx.data_ptr(),
-           tuple(w.data_ptr() for w in weights))
+    bufs = (x_buf, x_out_buf, att_xx, aa, bb, pp, ffn_xx)
+    key = (int(layer_id), tuple((t.data_ptr(), tuple(t.shape)) for t in bufs),
+           tuple((w.data_ptr(), tuple(w.shape)) for w in weights))
     hit = _LAYER_GRAPHS.get(key)
     if hit is None:
         L, C, F, keep = _layer_struct(x_buf, att_xx, aa, bb, pp, ffn_xx, *weights)

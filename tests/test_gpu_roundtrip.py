@@ -102,6 +102,29 @@ def test_decode_groups_and_graph_agree(eng):
             np.testing.assert_array_equal(d, t)
 
 
+@pytest.mark.parametrize("layer", [5, 11])
+def test_graph_decode_with_an_unpacked_later_layer(eng, layer):
+    """A layer with no fragment-packed weights runs on the unfused small-M
+    path, which writes the workspace rows and buffer that the graph decode's
+    layer-0 LN1-mix fold keeps its carried rows and its argument block in.
+    The fold must then stay off: the graph and the eager decode of such a
+    model both give back the tokens (every path keeps the same bits)."""
+    toks = [synthetic.zipf_tokens(1, n, seed_base=4100 + i)[0] for i, n in enumerate([30, 9, 22, 1])]
+    enc = eng.compress_tokens_batched(toks)
+    L = eng.weights["prepared"].layers_c[layer]
+    saved = (L.Kf, L.fVf)
+    L.Kf, L.fVf = None, None
+    try:
+        for graph in (True, False):
+            eng.use_graph = graph
+            dec = eng.decompress_tokens_batched(enc)
+            for t, d in zip(toks, dec):
+                np.testing.assert_array_equal(d, t, err_msg=f"graph={graph}, layer {layer} unpacked")
+    finally:
+        L.Kf, L.fVf = saved
+        eng.use_graph = True
+
+
 def test_repeated_spans_roundtrip(eng):
     toks = synthetic.zipf_tokens(3, 640, repeat_rate=0.3)
     enc = eng.compress_tokens_batched(list(toks))
