@@ -120,19 +120,22 @@ class InferenceEngine:
 
     # ------------------------------------------------------------------ setup
     def load(self, weights: Optional[dict] = None, tokenizer_path: Optional[str] = None,
-             device: str = "cuda", w8a8: bool = False):
+             device: str = "cuda", w8a8: bool = False, rescale: bool = True):
         """Prepare weights and an optional tokenizer. `weights` is a dict in
         the engine layout (rwkv-package keys, [in, out] matrices, raw
         time_decay), a path to an RWKV-4 `.pth` / `.safetensors` checkpoint
         (converted by krunch_amd.weights.load_rwkv4), or None for the
         synthetic RWKV-4-169M-shaped model (seed 0). w8a8=True selects the
-        int8 codec (model_id 2): its streams decode only with the int8 codec."""
+        int8 codec (model_id 2): its streams decode only with the int8 codec.
+        rescale applies to checkpoint paths only (krunch_amd.weights): True,
+        the default, computes what the reference codec computes on that
+        checkpoint."""
         if weights is None:
             from krunch_amd.synthetic import make_weights
             weights = make_weights()
         elif isinstance(weights, (str, os.PathLike)):
             from krunch_amd.weights import load_rwkv4
-            weights = load_rwkv4(weights)
+            weights = load_rwkv4(weights, rescale=rescale)
         self._weights = cpp_path.init_weights(weights, device, w8a8=w8a8)
         self.model_id = MODEL_ID_W8A8 if w8a8 else MODEL_ID
         from krunch_amd.tokenizer import load_tokenizer

@@ -20,13 +20,19 @@ layout needs:
 * matrices, embedding, LayerNorm and mix vectors become fp16; time_decay and
   time_first stay fp32.
 
-RESCALE: for fp16 the rwkv package divides `att.output.weight` and
-`ffn.value.weight` of layer i by 2^(i // 6) and halves x after every sixth
-layer in its own forward. The reference's C++ path uses those rescaled
-weights but never halves x (layer_cpp.cpp:456-637). The engine computes the
-unscaled model, so the default here is `rescale=False` (weights as in the
-checkpoint); `rescale=True` reproduces the package's weights for comparisons
-against the reference's numbers.
+RESCALE: for fp16 strategies ('cuda fp16', the one inference.py:186 picks on
+a GPU) the rwkv package divides `att.output.weight` and `ffn.value.weight`
+of layer i by 2^(i // 6) at load time, and its own forward halves x after
+every sixth layer, so that the package computes the unscaled model. The
+reference's codec takes those rescaled weights (`model.w`,
+cpp_path.py:26-91) into a layer path that never halves x
+(cpp_path.py:131-163, layer_cpp.cpp:456-637): on a real checkpoint the
+reference compresses with "rescaled weights, x never halved", which differs
+from the unscaled model in layers 6 and up. The default here is therefore
+`rescale=True`, so that the engine computes the reference codec's function
+on the same checkpoint (its bits/token and bitstreams are the reference's,
+up to rounding); `rescale=False` gives the unscaled model, which no
+reference stream was coded with.
 
 Checkpoints are read with `torch.load(..., weights_only=True)` or
 safetensors, which execute nothing from the file.
@@ -54,7 +60,7 @@ def _n_layer(sd: Mapping[str, torch.Tensor]) -> int:
     return n
 
 
-def convert_rwkv4_state_dict(sd: Mapping[str, torch.Tensor], rescale: bool = False,
+def convert_rwkv4_state_dict(sd: Mapping[str, torch.Tensor], rescale: bool = True,
                              rescale_layer: int = 6) -> Dict[str, torch.Tensor]:
     """RWKV-4 checkpoint tensors -> the engine's weight dict (CPU tensors)."""
     sd = {k: (v if isinstance(v, torch.Tensor) else torch.as_tensor(v)) for k, v in sd.items()}
@@ -95,7 +101,7 @@ def convert_rwkv4_state_dict(sd: Mapping[str, torch.Tensor], rescale: bool = Fal
     return out
 
 
-def load_rwkv4(path: str, rescale: bool = False) -> Dict[str, torch.Tensor]:
+def load_rwkv4(path: str, rescale: bool = True) -> Dict[str, torch.Tensor]:
     """Load an RWKV-4 checkpoint (`.pth` or `.safetensors`) into the engine's
     weight dict. `.pth` files are read with weights_only=True."""
     path = os.fspath(path)

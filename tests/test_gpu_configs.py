@@ -17,7 +17,7 @@ import torch
 
 from krunch_amd import cpp_path, synthetic
 from krunch_amd import krunch_ac_hip as ops
-from krunch_amd.inference import InferenceEngine
+from krunch_amd.inference import CDF_PRECISION, InferenceEngine
 from oracle import range_coder as orc
 from oracle import rwkv4
 from oracle import softmax as osm
@@ -143,16 +143,78 @@ def test_config5_three_windows_with_repeats(eng, w16):
     assert err < 1e-2, f"config 5 logits vs fp32 oracle after 3 windows: max abs {err}"
 
 
-def test_config5_full_length_chunks(eng):
-    """Config 5's chunk length: 8 chunks of 262,144 tokens each (256 windows,
-    5% repeats), compressed with state carried across every window and
-    decoded in 262,144 lockstep steps: byte-exact. (The decode step is
-    latency-bound, so 8 streams take about as long as 256 would per step.)"""
-    B, T = 8, 262144
+def _decode_in_calls(eng, enc, calls, report):
+    """Lockstep decode of every stream through kr_decode_run, split into
+    `calls` calls of equal step counts (the state, coder state and decoded
+    symbols carry over; split calls give the bits of one call). Returns
+    [B, Tmax] int32 tokens on the host."""
+    import struct
+    from krunch_amd import _lib
+    from krunch_amd.model import State
+    P = eng.weights["prepared"]
+    B = len(enc)
+    n_tok = [struct.unpack(">II", e[:8])[1] for e in enc]
+    streams = [e[8:] for e in enc]
+    offs = np.cumsum([0] + [len(s) for s in streams])
+    inbuf = torch.from_numpy(np.frombuffer(b"".join(streams) + b"\0", dtype=np.uint8).copy()).to(DEV)
+    base = torch.from_numpy(offs[:-1].astype(np.int32)).to(DEV)
+    limits = torch.tensor([len(s) for s in streams], dtype=torch.int32, device=DEV)
+    ac = torch.empty((B, 4), dtype=torch.uint32, device=DEV)
+    s = _lib.stream_ptr()
+    _lib.call("kr_decode_init_batched", inbuf.data_ptr(), inbuf.numel(), base.data_ptr(),
+              limits.data_ptr(), ac.data_ptr(), B, s)
+    Tmax = max(n_tok)
+    state = State(P.n_layer, B, P.C, DEV)
+    syms = torch.zeros(B, dtype=torch.int32, device=DEV)
+    tokens = torch.zeros((B, Tmax), dtype=torch.int32, device=DEV)
+    count = torch.zeros(B, dtype=torch.int32, device=DEV)
+    ntd = torch.tensor(n_tok, dtype=torch.int32, device=DEV)
+    x = torch.empty((B, P.C), dtype=torch.float16, device=DEV)
+    nbytes = _lib.lib().kr_decode_workspace_bytes(B, 1, P.C, P.F)
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=DEV)
+    ld = cpp_path.logits_ld(P.V)
+    logits = torch.empty((B, ld), dtype=torch.float16, device=DEV)
+    step = (Tmax + calls - 1) // calls
+    for c in range(calls):
+        n = min(step, Tmax - c * step)
+        _lib.call("kr_decode_run", P.ptr, B, state.ptr, syms.data_ptr(), x.data_ptr(),
+                  ws.data_ptr(), nbytes, logits.data_ptr(), ld, inbuf.data_ptr(), inbuf.numel(),
+                  base.data_ptr(), limits.data_ptr(), ac.data_ptr(), tokens.data_ptr(), Tmax,
+                  count.data_ptr(), ntd.data_ptr(), CDF_PRECISION, n, 1, 1, s)
+        torch.cuda.synchronize()
+        report(f"decoded {(c + 1) * step if c + 1 < calls else Tmax} of {Tmax} steps")
+    assert torch.equal(count.cpu(), ntd.cpu())
+    return tokens.cpu().numpy()
+
+
+def test_config5_whole(eng, capsys):
+    """Config 5 whole: 256 chunks of 262,144 tokens (5% repeated 64-token
+    spans), compressed in 256 windows of 1024 tokens with the state carried
+    across windows, then decoded in 262,144 lockstep steps of 256 streams:
+    byte-exact. The first 3,072 tokens of one stream's payload equal the
+    oracle coder fed the oracle CDF of that stream's GPU logits (the bits a
+    range coder has emitted after n symbols do not depend on later symbols,
+    so the whole stream's prefix equals the n-symbol stream's, short of the
+    final flush). Progress lines go straight to the terminal: the test runs
+    for about three minutes."""
+    def report(msg):
+        with capsys.disabled():
+            print(f"[config 5 whole] {msg}", flush=True)
+    B, T = 256, 262144
     toks = synthetic.zipf_tokens(B, T, repeat_rate=0.05, seed_base=5500)
+    report("tokens drawn; compressing")
     enc = eng.compress_tokens_batched(list(toks))
-    dec = eng.decompress_tokens_batched(enc)
-    for t, d in zip(toks, dec):
-        np.testing.assert_array_equal(d, t)
     bpt = 8 * sum(len(e) - 8 for e in enc) / (B * T)
+    report(f"compressed: {bpt:.3f} bits/token")
     assert 8.0 < bpt < 17.0, bpt
+    b, n = 97, 3072
+    st = cpp_path.fresh_state_batched(eng.weights, 1)
+    got = cpp_path.forward_packed_batched(eng.weights, synthetic.model_inputs(toks[b:b + 1, :n]), st)
+    ref = orc.encode(osm.logits_to_cdf(got.cpu().numpy()), toks[b, :n])
+    # the n-symbol stream ends with a flush of pending + 2 bits and a partial
+    # byte: 8 bytes cover it unless 55 E3 steps were pending at once
+    keep = len(ref) - 8
+    assert enc[b][8:8 + keep] == ref[:keep], "stream 97: payload prefix differs from the oracle chain"
+    dec = _decode_in_calls(eng, enc, 8, report)
+    for i in range(B):
+        np.testing.assert_array_equal(dec[i], toks[i], err_msg=f"stream {i}")

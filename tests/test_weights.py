@@ -51,7 +51,7 @@ def test_layout_and_ln0_fold():
 
 def test_rescale():
     sd = _ckpt(n_layer=8)
-    w0, w1 = convert_rwkv4_state_dict(sd), convert_rwkv4_state_dict(sd, rescale=True)
+    w0, w1 = convert_rwkv4_state_dict(sd, rescale=False), convert_rwkv4_state_dict(sd, rescale=True)
     for i in (0, 5, 6, 7):
         s = 2 ** (i // 6)
         for m in ("att.output.weight", "ffn.value.weight"):
@@ -82,3 +82,54 @@ def test_rejects_bad_checkpoints():
     sd["blocks.3.ln1.weight"] = sd["blocks.0.ln1.weight"]
     with pytest.raises(ValueError):
         convert_rwkv4_state_dict(sd)
+
+
+def test_default_is_the_reference_codecs_weights(tmp_path):
+    """The default conversion is the rescaled one (what the reference's codec
+    reads from the rwkv package's 'cuda fp16' model.w), also through a file."""
+    sd = _ckpt(n_layer=8)
+    w = convert_rwkv4_state_dict(sd)
+    wr = convert_rwkv4_state_dict(sd, rescale=True)
+    assert all(torch.equal(w[k], wr[k]) for k in w)
+    assert torch.equal(w["blocks.7.att.output.weight"], (sd["blocks.7.att.output.weight"].t() / 2).half())
+    torch.save(sd, tmp_path / "m.pth")
+    back = load_rwkv4(str(tmp_path / "m.pth"))
+    assert all(torch.equal(back[k], wr[k]) for k in w)
+
+
+def _forward(w, ids, halve_every=0):
+    """oracle.rwkv4's forward, optionally halving x after every
+    `halve_every`-th layer (the rwkv package's own fp16 forward)."""
+    from oracle import rwkv4
+    n_layer = 1 + max(int(k.split(".")[1]) for k in w if k.startswith("blocks."))
+    C = w["emb.weight"].shape[1]
+    state = rwkv4.new_state(n_layer, ids.shape[0], C)
+    f = {k: v.float() for k, v in w.items()}
+    x = f["emb.weight"][ids]
+    with torch.no_grad():
+        for i, st in enumerate(state):
+            x = rwkv4.time_mix(x, st, f, i, False)
+            x = rwkv4.channel_mix(x, st, f, i, False)
+            if halve_every and (i + 1) % halve_every == 0:
+                x = x / 2
+        x = torch.nn.functional.layer_norm(x, (C,), f["ln_out.weight"], f["ln_out.bias"], 1e-5)
+        return (x @ f["head.weight"]).numpy()
+
+
+def test_rescale_convention_and_what_it_changes():
+    """What pins the rescale rule (2^(i // 6) on att.output / ffn.value):
+    the rwkv package's own forward, which halves x after every sixth layer,
+    computes on rescaled weights what the unscaled weights compute without
+    halving (LayerNorm ignores the scale of its input up to eps). A rule off
+    by one layer breaks that. The reference codec's function (rescaled
+    weights, x never halved; the engine's default) is a different model in
+    layers 6 and up."""
+    sd = _ckpt(n_layer=12, C=256, F=512, V=300, seed=9)
+    plain = convert_rwkv4_state_dict(sd, rescale=False)
+    scaled = convert_rwkv4_state_dict(sd, rescale=True)
+    ids = torch.as_tensor(np.random.default_rng(3).integers(0, 300, (2, 12)))
+    ref = _forward(plain, ids)
+    assert np.abs(_forward(scaled, ids, halve_every=6) - ref).max() < 1e-3
+    wrong = convert_rwkv4_state_dict(sd, rescale=True, rescale_layer=5)
+    assert np.abs(_forward(wrong, ids, halve_every=6) - ref).max() > 1e-2
+    assert np.abs(_forward(scaled, ids) - ref).max() > 1e-2
