@@ -51,6 +51,13 @@ def parse():
     ap.add_argument("--hbm-table", metavar="CSV",
                     help="print the per-kernel HBM fraction of a decode step from a rocprofv3 "
                          "kernel-trace CSV of this bench (no GPU work)")
+    ap.add_argument("--roofline-json", metavar="OUT",
+                    help="with --hbm-table: also write the in-step durations of the two "
+                         "roofline launches to OUT (bench.py reads profiles/"
+                         "decode_step_B256_roofline.json for its roofline lines)")
+    ap.add_argument("--bench-line", metavar="JSON",
+                    help="with --roofline-json: the bench line printed by the profiled run, "
+                         "whose live in-step wave spans are recorded beside the trace figures")
     ap.add_argument("--kernel-probe", action="store_true",
                     help="only run a 256 MiB device copy (counter calibration), 8 launches of "
                          "the dominant kernel and 2 eager launches of each other hot kernel at "
@@ -169,7 +176,7 @@ def kernel_probe(weights16, B):
     print(json.dumps({"probe": "ok", "copy_bytes": 2 * src.numel() * 4}))
 
 
-def gpu_bench(args, weights16, w8a8=False):
+def gpu_bench(args, weights16, w8a8=False, step_probe=False):
     import numpy as np
     import torch
     from krunch_amd import _lib, cpp_path, synthetic
@@ -180,13 +187,17 @@ def gpu_bench(args, weights16, w8a8=False):
     P = W["prepared"]
     B, Tw = args.batch, args.window
     n_win = args.warmup + args.steps
-    L = n_win * Tw
+    # one more window after the timed ones: compressed untimed, and the first
+    # probe_steps of its decode run with the decode-step timing on
+    # (step_timed_launches), so that measurement never touches the timed region
+    probe_steps = PROBE_STEPS if step_probe else 0
+    L = (n_win + (1 if step_probe else 0)) * Tw
     toks = synthetic.zipf_tokens(B, L, repeat_rate=0.05)
     inp = synthetic.model_inputs(toks)
     tok_d = torch.from_numpy(toks).to(dev)
     inp_d = torch.from_numpy(inp).to(dev)
-    win_inp = [inp_d[:, w * Tw:(w + 1) * Tw].contiguous() for w in range(n_win)]
-    win_tok = [tok_d[:, w * Tw:(w + 1) * Tw].contiguous() for w in range(n_win)]
+    win_inp = [inp_d[:, w * Tw:(w + 1) * Tw].contiguous() for w in range(L // Tw)]
+    win_tok = [tok_d[:, w * Tw:(w + 1) * Tw].contiguous() for w in range(L // Tw)]
     s = _lib.stream_ptr()
     PREC = 24
 
@@ -235,6 +246,8 @@ def gpu_bench(args, weights16, w8a8=False):
         compress_window(w)
     torch.cuda.synchronize()
     t_c = time.perf_counter() - t0
+    for w in range(n_win, L // Tw):
+        compress_window(w)
     main.wait_stream(enc)
     _lib.call("kr_encode_finalize_batched", out.data_ptr(), out.numel(), base.data_ptr(),
               ac.data_ptr(), B, err.data_ptr(), s)
@@ -258,11 +271,11 @@ def gpu_bench(args, weights16, w8a8=False):
     dtoks = torch.zeros((B, L), dtype=torch.int32, device=dev)
     cnt = torch.zeros(B, dtype=torch.int32, device=dev)
 
-    def decode(n_steps):
+    def decode(n_steps, graph=True):
         _lib.call("kr_decode_run", P.ptr, B, dstate.ptr, syms.data_ptr(), dx.data_ptr(),
                   dws.data_ptr(), dws_bytes, dlogits.data_ptr(), ld, out.data_ptr(), out.numel(),
                   base.data_ptr(), nbytes.data_ptr(), dac.data_ptr(), dtoks.data_ptr(), L,
-                  cnt.data_ptr(), None, PREC, n_steps, G, 1, s)
+                  cnt.data_ptr(), None, PREC, n_steps, G, 1 if graph else 0, s)
 
     if args.warmup:
         decode(args.warmup * Tw)
@@ -271,12 +284,67 @@ def gpu_bench(args, weights16, w8a8=False):
     decode(args.steps * Tw)
     torch.cuda.synchronize()
     t_d = time.perf_counter() - t0
-    exact = bool(torch.equal(dtoks, tok_d))
+    in_step, used = step_timed_launches(decode, probe_steps) if step_probe else (None, 0)
+    n_dec = n_win * Tw + used
+    exact = bool(torch.equal(dtoks[:, :n_dec], tok_d[:, :n_dec]))
     if not exact:
-        bad = (dtoks != tok_d).nonzero()
+        bad = (dtoks[:, :n_dec] != tok_d[:, :n_dec]).nonzero()
         raise SystemExit(f"round trip NOT byte-exact; first mismatch (stream, token) = {bad[0].tolist()}")
     ntok = args.steps * B * Tw
-    return dict(t_c=t_c, t_d=t_d, ntok=ntok, comp_bytes=comp_bytes, total_tok=B * L, exact=exact)
+    return dict(t_c=t_c, t_d=t_d, ntok=ntok, comp_bytes=comp_bytes, total_tok=B * L, exact=exact,
+                in_step=in_step)
+
+
+# Decode-step phases (kr_phase_name) of the two roofline kernels, and the
+# decode steps step_timed_launches runs after the timed region.
+PHASE_FFN_RK, PHASE_FFN_V = 5, 6
+PROBE_STEPS = 64
+
+
+def step_timed_launches(decode, n_steps, calls=4):
+    """In-step durations of the two roofline launches, from decode steps that
+    continue the timed region's streams (the same kernels, state and
+    bitstreams), with the channel-mix R + K launch (then the value-product
+    launch) of every layer timed (kr_step_timing):
+      * "events": eager steps, the timed launch through hipExtLaunchKernel
+        with two HIP events that take its dispatch's start and end (the
+        times a kernel trace reports). A bounded GPU sleep is queued first,
+        so the host enqueues the steps ahead of the GPU and the launches run
+        back to back, as a replayed graph runs them;
+      * "span": graph-replayed steps exactly as timed, each launch's last
+        wave end minus its first wave start on the 100 MHz steady counter
+        (dispatch and teardown not included).
+    Each call of n_steps / (4 * calls) steps yields one sample per layer,
+    from its last step. Returns ({phase: {"events": [us...], "span": [us...],
+    "span_eager": [us...]}}, steps decoded)."""
+    import ctypes
+    import torch
+    from krunch_amd import _lib
+    per_call = max(1, n_steps // (4 * calls))
+    used = 0
+    out = {}
+    launch = (ctypes.c_double * 64)()
+    span = (ctypes.c_double * 64)()
+    got = ctypes.c_int(0)
+    try:
+        for phase in (PHASE_FFN_RK, PHASE_FFN_V):
+            _lib.call("kr_step_timing", phase, None)
+            r = {"events": [], "span": [], "span_eager": []}
+            for graph in (True, False):
+                for _ in range(calls):
+                    if not graph:
+                        torch.cuda._sleep(20_000_000)     # ~10 ms of GPU clock cycles
+                    decode(per_call, graph)
+                    used += per_call
+                    _lib.call("kr_step_timing_read", launch, span, 64, ctypes.byref(got))
+                    n = got.value
+                    r["span" if graph else "span_eager"] += [span[i] for i in range(n)]
+                    if not graph:
+                        r["events"] += [launch[i] for i in range(n)]
+            out[phase] = r
+    finally:
+        _lib.lib().kr_step_timing(-1, None)
+    return out, used
 
 
 def _pack(X):
@@ -314,20 +382,55 @@ def _graph_launch_us(launches):
     return min(ms[1:]) * 1000.0 / n
 
 
-def _roofline_entry(kernel, alg_bytes, us, traffic_file, B):
+ROOFLINE_TRACE = os.path.join(ROOT, "profiles", "decode_step_B256_roofline.json")
+
+
+def _roofline_entry(kernel, alg_bytes, us_isolated, step, phase_key, traffic_file, B):
+    """`frac` from the launch's average duration inside the decode step as a
+    kernel trace of this bench measures it (dispatch to completion; recorded
+    by `bench.py --hbm-table ... --roofline-json` in ROOFLINE_TRACE, at B =
+    256). Beside it, measured live in this run: the launch's in-step wave span
+    (step_timed_launches; the trace file records the span of the profiled
+    run, so `trace_matches_build` says whether this build runs the launch as
+    the traced one did, within 5%) and the isolated HIP-event figure."""
     traffic = None
     tfile = os.path.join(ROOT, "profiles", traffic_file)
     if os.path.exists(tfile) and B == 256:
         with open(tfile) as f:
             traffic = json.load(f).get("hbm_bytes_per_launch")
-    achieved = alg_bytes / (us * 1e-6) / 1e9
-    return {"kernel": kernel, "bound": "hbm", "achieved": round(achieved, 2),
-            "peak": MI355X_HBM_PEAK / 1e9, "unit": "GB/s",
-            "frac": round(achieved / (MI355X_HBM_PEAK / 1e9), 4), "traffic": traffic,
-            "alg_bytes_per_launch": alg_bytes, "avg_launch_us": round(us, 3)}
+    peak = MI355X_HBM_PEAK / 1e9
+    gbs = lambda us: alg_bytes / (us * 1e-6) / 1e9
+    mean = lambda v: sum(v) / len(v)
+    trace = None
+    if B == 256 and os.path.exists(ROOFLINE_TRACE):
+        with open(ROOFLINE_TRACE) as f:
+            trace = json.load(f)["phases"].get(phase_key)
+    span = mean(step["span"]) if step and step.get("span") else None
+    if trace:
+        us = trace["in_step_mean_us"]
+        timing = ("in the decode step: mean duration of the %d launches of this kernel inside "
+                  "the decode steps of a rocprofv3 kernel trace of this bench (%s)"
+                  % (trace["launches"], os.path.relpath(ROOFLINE_TRACE, ROOT)))
+    else:
+        us = us_isolated
+        timing = "isolated: graph of 64 launches over 64 weight copies"
+    out = {"kernel": kernel, "bound": "hbm", "achieved": round(gbs(us), 2), "peak": peak,
+           "unit": "GB/s", "frac": round(gbs(us) / peak, 4), "traffic": traffic,
+           "alg_bytes_per_launch": alg_bytes, "avg_launch_us": round(us, 3), "timing": timing,
+           "isolated": {"avg_launch_us": round(us_isolated, 3),
+                        "achieved": round(gbs(us_isolated), 2),
+                        "frac": round(gbs(us_isolated) / peak, 4)}}
+    if step:
+        out["in_step_wave_span_us"] = {"graph": round(span, 3),
+                                       "eager": round(mean(step["span_eager"]), 3),
+                                       "eager_dispatch_events": round(mean(step["events"]), 3)}
+    if trace and span and trace.get("wave_span_us_same_run"):
+        ref = trace["wave_span_us_same_run"]
+        out["trace_matches_build"] = bool(abs(span / ref - 1) <= 0.05)
+    return out
 
 
-def dominant_kernel_roofline(weights16, B):
+def dominant_kernel_roofline(weights16, B, in_step=None):
     """Live rooflines of the two heaviest kernels of the timed region, both
     stepped small-M products of the decode step (12 launches each per step),
     HBM-bound:
@@ -338,10 +441,14 @@ def dominant_kernel_roofline(weights16, B):
       * the channel-mix value product (M = B, K = 3072, N = 768, gated
         residual), W 3072 * 768 * 2 + A B * 3072 * 2 + residual, gate and
         output 3 * B * 768 * 2.
-    Each is launched exactly as the decode step launches it (fragment-packed
-    operands), in a captured graph of 64 launches over 64 distinct weight
-    copies (> the 256 MB memory-side cache, so weights come from HBM as in a
-    real step), timed with HIP events on the replay stream. `traffic` is the
+    `frac` comes from each launch's average duration inside the decode step
+    in a kernel trace of this bench (ROOFLINE_TRACE), with the live in-step
+    wave span and the isolated figure beside it (_roofline_entry). The
+    isolated figure: the launch as the decode step launches it
+    (fragment-packed operands), in a captured
+    graph of 64 launches over 64 distinct weight copies (> the 256 MB
+    memory-side cache, so weights come from HBM), timed with HIP events on
+    the replay stream. `traffic` is the
     HBM bytes per launch from the committed counter summaries
     (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE on bench.py --kernel-probe,
     scaled by a 256 MiB copy calibration)."""
@@ -395,14 +502,15 @@ def dominant_kernel_roofline(weights16, B):
     us_v = _graph_launch_us(fv)
     del WV
     bytes_v = F * C * 2 + M * F * 2 + 3 * M * C * 2
+    in_step = in_step or {}
     top = _roofline_entry(
         "gemm_panel_kernel (stepped channel-mix R + K products in one launch, "
         "M=%d K=768 N=768 sigmoid + 3072 relu^2, fragment-packed operands; top kernel by time)" % M,
-        bytes_rk, us_rk, "gemm_panel_ffn_rk_B256_traffic.json", B)
+        bytes_rk, us_rk, in_step.get(PHASE_FFN_RK), "rk", "gemm_panel_ffn_rk_B256_traffic.json", B)
     second = _roofline_entry(
         "gemm_panel_kernel (stepped channel-mix value product, M=%d K=3072 N=768, "
         "gated residual, fragment-packed operands; second by time)" % M,
-        bytes_v, us_v, "gemm_panel_ffn_value_B256_traffic.json", B)
+        bytes_v, us_v, in_step.get(PHASE_FFN_V), "fv", "gemm_panel_ffn_value_B256_traffic.json", B)
     return top, second
 
 
@@ -459,7 +567,7 @@ def step_phases(names):
     return out
 
 
-def hbm_table(csv_path, B):
+def hbm_table(csv_path, B, roofline_json=None, bench_line=None):
     """Per-phase HBM fraction of one decode step from a rocprofv3 kernel
     trace of the bench (markdown on stdout): each phase's algorithmic bytes
     per launch over its median duration in the trace's decode steps (the
@@ -494,6 +602,32 @@ def hbm_table(csv_path, B):
               f"{gbs / (MI355X_HBM_PEAK / 1e9):.3f} | {us * per_step:.1f} |")
     print(f"\nSum over the step: {total:.1f} us (median launches; the profiler adds ~1 us per "
           f"kernel).")
+    if roofline_json:
+        # in-step durations (every launch of the phase inside the trace's
+        # decode steps) of the two roofline kernels
+        out = {"trace": os.path.basename(csv_path), "batch": B, "phases": {}}
+        spans = {}
+        if bench_line:
+            with open(bench_line) as f:
+                line = json.loads(f.read().strip().splitlines()[-1])
+            for key, name in (("rk", "roofline"), ("fv", "roofline_second_kernel")):
+                span = line.get(name, {}).get("in_step_wave_span_us")
+                if span:
+                    spans[key] = span["graph"]
+        for key in ("rk", "fv"):
+            if key not in durs:
+                continue
+            kn = max(durs[key], key=lambda k: len(durs[key][k]))
+            # the timed decode's steps: the last PROBE_STEPS steps of the trace
+            # are step_timed_launches' (12 launches each), not the timed region's
+            d = sorted(durs[key][kn][:-12 * PROBE_STEPS])
+            name = kn[0].replace("(anonymous namespace)::", "").replace("void ", "").split("(")[0]
+            out["phases"][key] = {
+                "kernel": name, "grid": kn[1], "launches": len(d),
+                "in_step_mean_us": round(sum(d) / len(d), 4), "in_step_median_us": d[len(d) // 2],
+                "wave_span_us_same_run": spans.get(key)}
+        with open(roofline_json, "w") as f:
+            json.dump(out, f, indent=1)
 
 
 def cpu_baseline(args):
@@ -549,7 +683,7 @@ def main():
               file=sys.stderr)
         sys.exit(2)
     if args.hbm_table:
-        hbm_table(args.hbm_table, args.batch)
+        hbm_table(args.hbm_table, args.batch, args.roofline_json, args.bench_line)
         return
     import torch
     from krunch_amd import synthetic
@@ -557,7 +691,7 @@ def main():
     if args.kernel_probe:
         kernel_probe(weights16, args.batch)
         return
-    r = gpu_bench(args, weights16)
+    r = gpu_bench(args, weights16, step_probe=True)
     t = r["t_c"] + r["t_d"]
     kb = r["ntok"] * BYTES_PER_TOKEN / 1024
     res = {
@@ -603,7 +737,8 @@ def main():
             "roundtrip_exact": q["exact"],
             "compress_int8_fp16_tops": round(q["ntok"] * FLOP_PER_TOKEN / q["t_c"] / 1e12, 1),
         }
-    res["roofline"], res["roofline_second_kernel"] = dominant_kernel_roofline(weights16, args.batch)
+    res["roofline"], res["roofline_second_kernel"] = dominant_kernel_roofline(
+        weights16, args.batch, r["in_step"])
     if not args.no_cpu_baseline:
         res["cpu_baseline"] = cpu_baseline(args)
     print(json.dumps(res))

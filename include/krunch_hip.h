@@ -308,6 +308,22 @@ const char* kr_phase_name(int i);
 int kr_read_phase_times(double* ms, int n, long long* call_count);
 int kr_reset_phase_times(void);
 
+/* Decode-step timing, the same profiler's role (layer_cpp.cpp:111-157) for
+ * the stepped decode. kr_step_timing(p) with p = 3 (ow_matmul_residual),
+ * 5 (ffn_rk_matmul) or 6 (ffn_v_matmul_residual) times that phase's product
+ * in every layer of every later decode step (kr_decode_step, kr_decode_run,
+ * graph or eager): each of its waves stores its start and end on the GPU's
+ * 100 MHz steady counter (a vector store per wave, also at every replay of a
+ * captured graph), and in eager steps the launch goes through
+ * hipExtLaunchKernel with two HIP events that take its dispatch's start and
+ * end. Nothing else in the step changes. p = -1 turns it off; *previous
+ * (nullable) receives the earlier setting. kr_step_timing_read waits for the
+ * device and writes, for layers 0 .. n_read - 1 of the last timed step
+ * (n_read = min(n, layers)), the launch's event duration (-1 for a graph
+ * step) and its wave span (last wave end minus first wave start), in
+ * microseconds; it fails if no timed step ran since the last reading. */
+int kr_step_timing_read(double* launch_us, double* span_us, int n, int* n_read);
+
 /* replaces launch_krunch_wkv_forward (wkv_kernel.cu:75-92), fused with the
  * receptance: ry = fp16(r * fp16(y)); k, v fp32 [B*T, C], r/ry fp16. */
 int kr_wkv(int B, int T, int C, const float* decay, const float* first, const float* k,

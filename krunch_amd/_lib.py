@@ -85,6 +85,9 @@ _SIGS = {
     "kr_phase_name": ([I], ctypes.c_char_p),
     "kr_read_phase_times": ([ctypes.POINTER(ctypes.c_double), I, ctypes.POINTER(LL)], I),
     "kr_reset_phase_times": ([], I),
+    "kr_step_timing": ([I, ctypes.POINTER(I)], I),
+    "kr_step_timing_read": ([ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double), I,
+                             ctypes.POINTER(I)], I),
     "kr_forward_layers": ([ctypes.POINTER(KrModelWeights), P, I, I, P, P, SZ, P], I),
     "kr_embed": ([ctypes.POINTER(KrModelWeights), P, I, P, P], I),
     "kr_head_logits": ([ctypes.POINTER(KrModelWeights), P, I, P, P, LL, P], I),

@@ -91,6 +91,9 @@ struct kr_gemm_multi {
     int ep[KR_GEMM_MAX_JOBS];
     int tiles[KR_GEMM_MAX_JOBS];
     int njobs;
+    // decode-step timing (null otherwise): wave w of workgroup b stores its
+    // start and end times (the 100 MHz steady counter) at stamps[16 b + w]
+    unsigned long long* stamps;
 };
 
 // Launch C = A @ W (W given transposed), kernel and tile shape chosen from M.
@@ -101,6 +104,23 @@ struct kr_gemm_multi {
 // then the epilogue. A row therefore gets identical bits for any M. The int8
 // path accumulates exactly in int32, so any order gives the same bits.
 int kr_gemm_launch(const kr_gemm_args& g, int epilogue, hipStream_t stream);
+
+// Kernel timing for the decode-step profiler: the next small-M panel launch
+// on this host thread (kr_gemm_launch / kr_gemm_launch_multi choosing
+// gemm_panel_kernel) with at most max_groups workgroups gets `stamps`
+// (2 x KR_STAMP_WAVES x max_groups u64, see kr_gemm_multi) and stores each
+// wave's start and end times there, also when it is captured in a graph
+// (then at every replay). Arm with a buffer, disarm with nullptr.
+// kr_gemm_timed_launch_taken(): the grid size of the panel launch that took
+// the buffer since it was armed; 0 if none came; minus the grid size if one
+// came with more than max_groups workgroups (it ran untimed).
+// With start / stop events as well (an eager launch; not under stream
+// capture) the launch goes through hipExtLaunchKernel, whose events take the
+// dispatch's own start and end times.
+constexpr int KR_STAMP_WAVES = 16;
+void kr_gemm_time_next_panel(unsigned long long* stamps, int max_groups,
+                             hipEvent_t start = nullptr, hipEvent_t stop = nullptr);
+int kr_gemm_timed_launch_taken();
 // Several products; on the small-M path those sharing M and K run in one
 // launch (independent outputs), otherwise they are launched in order.
 // Width (in 16-column panels) of the column groups the small-M fragment

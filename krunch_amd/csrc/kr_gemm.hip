@@ -18,6 +18,8 @@
 //    panels streamed, 8 MFMAs per (row block, panel); the slice partials are
 //    added in slice order through LDS and the epilogue is shared out over the
 //    waves. Parallelism comes from the K slices, not from M.
+#include <hip/hip_ext.h>
+
 #include <algorithm>
 #include <climits>
 #include <type_traits>
@@ -550,6 +552,15 @@ __global__ void __launch_bounds__(MAXT) gemm_panel_kernel(kr_gemm_multi mj) {
     typedef typename std::conditional<I8, kr_int4, kr_float4>::type Acc;
     extern __shared__ __attribute__((aligned(16))) float part_lds[];   // [S][TT][256]
     const int lane = threadIdx.x & 63, s = threadIdx.x >> 6;
+    // decode-step timing only (stamps non-null): this wave's start and end
+    const unsigned long long t_start = mj.stamps ? (unsigned long long)wall_clock64() : 0ull;
+    auto stamp_end = [&]() {
+        if (mj.stamps && lane == 0) {
+            typedef unsigned long long u64x2 __attribute__((ext_vector_type(2)));
+            *reinterpret_cast<u64x2*>(mj.stamps + 2 * (KR_STAMP_WAVES * blockIdx.x + s)) =
+                u64x2{t_start, (unsigned long long)wall_clock64()};
+        }
+    };
     // Job of this workgroup; fields are copied with constant indices so every
     // kernel-argument load is issued up front (no dependent scalar loads).
     const int bid = blockIdx.x;
@@ -807,6 +818,7 @@ __global__ void __launch_bounds__(MAXT) gemm_panel_kernel(kr_gemm_multi mj) {
             if constexpr (I8) epilogue(t, t, dequant(t, p[t / NS][t % NS]));
             else epilogue(t, t, p[t / NS][t % NS]);
         }
+        stamp_end();
         return;
     }
     #pragma unroll
@@ -821,6 +833,7 @@ __global__ void __launch_bounds__(MAXT) gemm_panel_kernel(kr_gemm_multi mj) {
         if constexpr (I8) epilogue(t, e, dequant(t, acc));
         else epilogue(t, e, acc);
     }
+    stamp_end();
 }
 
 template <int BM, int BN, bool I8>
@@ -844,6 +857,11 @@ struct PanelShape {
     int TM, NS;
 };
 
+thread_local unsigned long long* t_panel_stamps = nullptr;
+thread_local int t_panel_cap = 0;
+thread_local int t_panel_taken = 0;
+thread_local hipEvent_t t_panel_ev[2] = {};
+
 template <int TM, int NS, bool FRAG, int MAXT, bool I8, bool QA>
 int launch_panel(kr_gemm_multi mj, hipStream_t s) {
     const int S = mj.job[0].K / kKS;
@@ -855,10 +873,43 @@ int launch_panel(kr_gemm_multi mj, hipStream_t s) {
     }
     size_t lds = S > 1 ? (size_t)S * TM * NS * 256 * sizeof(float) : 0;
     if (QA && S > 1) lds += (size_t)S * TM * 16 * sizeof(float);
-    gemm_panel_kernel<TM, NS, FRAG, MAXT, I8, QA><<<total, dim3(64 * S), lds, s>>>(mj);
+    mj.stamps = nullptr;
+    hipEvent_t ev0 = nullptr, ev1 = nullptr;
+    if (t_panel_stamps) {
+        // the buffer holds KR_STAMP_WAVES slots for t_panel_cap workgroups
+        const bool fits = total <= t_panel_cap && S <= KR_STAMP_WAVES;
+        if (fits) {
+            mj.stamps = t_panel_stamps;
+            ev0 = t_panel_ev[0];
+            ev1 = t_panel_ev[1];
+        }
+        t_panel_stamps = nullptr;
+        t_panel_ev[0] = t_panel_ev[1] = nullptr;
+        t_panel_taken = fits ? total : -total;
+    }
+    if (ev0)
+        hipExtLaunchKernelGGL(gemm_panel_kernel<TM, NS, FRAG, MAXT, I8, QA>, dim3(total),
+                              dim3(64 * S), (uint32_t)lds, s, ev0, ev1, 0u, mj);
+    else
+        gemm_panel_kernel<TM, NS, FRAG, MAXT, I8, QA><<<total, dim3(64 * S), lds, s>>>(mj);
     KR_LAUNCHED();
     return KR_OK;
 }
+
+}  // namespace
+
+void kr_gemm_time_next_panel(unsigned long long* stamps, int max_groups, hipEvent_t start,
+                             hipEvent_t stop) {
+    t_panel_stamps = max_groups > 0 ? stamps : nullptr;
+    t_panel_cap = max_groups;
+    t_panel_taken = 0;
+    t_panel_ev[0] = t_panel_stamps && start && stop ? start : nullptr;
+    t_panel_ev[1] = t_panel_stamps && start && stop ? stop : nullptr;
+}
+
+int kr_gemm_timed_launch_taken() { return t_panel_taken; }
+
+namespace {
 
 // Shapes compiled per block size: up to 4 slices TM {1, 2, 4} x NS {1, 2};
 // up to 12 slices TM {1, 2} x NS {1, 2}; up to 16 slices TM 1 x NS {1, 2}.

@@ -632,12 +632,38 @@ bool kr_embed_mix_layer_ok(const kr_layer_weights& L, long long M, int T) {
 // ln1_mix, kvr_matmul, wkv, ow_matmul_residual, ln2_mix, ffn_rk_matmul,
 // ffn_v_matmul_residual. A fused launch that covers two phases leaves the
 // second one empty. ev == nullptr records nothing.
+// Marks lo .. lo + n - 1 are recorded, into ev[0 .. n - 1] (the layer
+// profiler records all eight; the decode-step timing only the two around
+// one phase).
+// stamps (the decode-step timing of phase lo, whose one launch must be a
+// small-M panel product): mark(lo) arms the buffer, and the events ev[0],
+// ev[1] when given, for that launch, which stores its waves' start and end
+// times there (the events take its dispatch's start and end); mark(lo + 1)
+// disarms them and puts the launch's grid size in *grid.
 struct Phases {
     hipEvent_t* ev = nullptr;
     hipStream_t s = nullptr;
+    int lo = 0, n = 8;
+    unsigned long long* stamps = nullptr;
+    int max_groups = 0;
+    int* grid = nullptr;
     int mark(int i) const {
-        if (!ev) return KR_OK;
-        KR_HIP(hipEventRecord(ev[i], s));
+        if (stamps) {
+            if (i == lo) {
+                kr_gemm_time_next_panel(stamps, max_groups, ev ? ev[0] : nullptr,
+                                        ev ? ev[1] : nullptr);
+            } else if (i == lo + 1) {
+                const int taken = kr_gemm_timed_launch_taken();
+                kr_gemm_time_next_panel(nullptr, 0);
+                KR_REQUIRE(taken != 0, "step timing: phase %d ran no small-M panel launch", lo);
+                KR_REQUIRE(taken > 0, "step timing: phase %d's launch has %d workgroups, more "
+                           "than the %d the timing buffer holds", lo, -taken, max_groups);
+                *grid = taken;
+            }
+            return KR_OK;
+        }
+        if (!ev || i < lo || i >= lo + n) return KR_OK;
+        KR_HIP(hipEventRecord(ev[i - lo], s));
         return KR_OK;
     }
 };
@@ -1034,6 +1060,34 @@ int profile_events() {
 }
 
 // ---------------------------------------------------------------------------
+// Decode-step timing: when a phase p whose launch is a small-M panel product
+// is selected (3 output projection, 5 channel-mix R + K, 6 value product),
+// every layer of a stepped forward launches that product with a stamp
+// buffer: each of its waves stores its start and end on the 100 MHz steady
+// counter (also inside a captured decode graph, at every replay). Outside
+// stream capture the launch also takes two HIP events through
+// hipExtLaunchKernel, which record its dispatch's start and end. Reading
+// returns, per layer, the last launch's event duration (eager steps) and its
+// wave span (last end minus first start), in microseconds. No other launch
+// changes.
+// ---------------------------------------------------------------------------
+constexpr int kMaxTimedLayers = 64;
+constexpr int kStampGroups = 2048;                 // workgroups per timed launch
+constexpr size_t kStampLayerU64 = 2ull * KR_STAMP_WAVES * kStampGroups;
+
+struct StepTiming {
+    std::mutex mu;
+    int phase = -1;                 // -1: off
+    int dev = -1;                   // device of `stamps` and `ev`
+    unsigned long long* stamps = nullptr;   // [kMaxTimedLayers][kStampLayerU64]
+    hipEvent_t ev[kMaxTimedLayers][2] = {};
+    int n = 0;                      // layers the last timed forward launched
+    bool eager = false;             // ... outside stream capture (events recorded)
+    int grid[kMaxTimedLayers] = {};
+};
+StepTiming g_step;
+
+// ---------------------------------------------------------------------------
 // Allocation-free layer step (kr_layer_step_noalloc): the workspace is this
 // file-scope device array, KR_NOALLOC_SCRATCH_BYTES per GPU, held until the
 // process ends. Host code never passes `scratch` itself (in host code the
@@ -1098,6 +1152,19 @@ int kr_impl_forward_layers_view(const kr_model_weights* m, void* x, int B, int T
     const size_t off = (size_t)b0 * m->C;
     KR_REQUIRE(!l0_mixed || ids, "forward: a mixed layer 0 needs the token ids");
     const EmbedSrc e{ids, H(m->emb), m->V, l0_mixed};
+    int tphase = -1;
+    if (T == 1) {
+        std::lock_guard<std::mutex> lock(g_step.mu);
+        int dev = 0;
+        KR_HIP(hipGetDevice(&dev));
+        if (g_step.phase >= 0 && g_step.stamps && g_step.dev == dev) {
+            tphase = g_step.phase;
+            g_step.n = std::min(m->n_layer, kMaxTimedLayers);
+            hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+            KR_HIP(hipStreamIsCapturing(s, &cs));
+            g_step.eager = cs == hipStreamCaptureStatusNone;
+        }
+    }
     for (int i = 0; i < m->n_layer; i++) {
         kr_layer_state st = state_of(state, i, state_B, m->C);
         st.att_xx = static_cast<kr_half*>(st.att_xx) + off;
@@ -1105,8 +1172,16 @@ int kr_impl_forward_layers_view(const kr_model_weights* m, void* x, int B, int T
         st.aa += off;
         st.bb += off;
         st.pp += off;
+        Phases ph;
+        if (tphase >= 0 && i < kMaxTimedLayers) {
+            ph.lo = tphase;
+            if (g_step.eager) ph.ev = g_step.ev[i];
+            ph.stamps = g_step.stamps + (size_t)i * kStampLayerU64;
+            ph.max_groups = kStampGroups;
+            ph.grid = &g_step.grid[i];
+        }
         KR_TRY(layer_forward(m->layers[i], m->C, m->F, Hm(x), B, T, st, w, s,
-                             i == 0 && ids ? &e : nullptr));
+                             i == 0 && ids ? &e : nullptr, ph));
     }
     return KR_OK;
 }
@@ -1318,6 +1393,73 @@ int kr_reset_phase_times(void) {
     std::lock_guard<std::mutex> lock(g_prof.mu);
     for (double& v : g_prof.sum_ms) v = 0.0;
     g_prof.calls = 0;
+    return KR_OK;
+}
+
+int kr_step_timing(int phase, int* previous) {
+    KR_REQUIRE(phase == -1 || phase == 3 || phase == 5 || phase == 6,
+               "kr_step_timing: phase %d is not a panel-product phase (3, 5 or 6)", phase);
+    std::lock_guard<std::mutex> lock(g_step.mu);
+    if (previous) *previous = g_step.phase;
+    if (phase >= 0) {
+        // the stamp buffer of the current device, cleared (slots of waves a
+        // launch does not have stay zero and are skipped when reading)
+        int dev = 0;
+        KR_HIP(hipGetDevice(&dev));
+        if (g_step.stamps && g_step.dev != dev) {
+            KR_REQUIRE(false, "kr_step_timing: already in use on device %d", g_step.dev);
+        }
+        const size_t bytes = (size_t)kMaxTimedLayers * kStampLayerU64 * 8;
+        if (!g_step.stamps) {
+            for (auto& pair : g_step.ev)
+                for (auto& e : pair) KR_HIP(hipEventCreate(&e));
+            void* p = nullptr;
+            KR_HIP(hipMalloc(&p, bytes));
+            g_step.stamps = static_cast<unsigned long long*>(p);
+            g_step.dev = dev;
+        }
+        KR_HIP(hipMemset(g_step.stamps, 0, bytes));
+    }
+    g_step.phase = phase;
+    g_step.n = 0;
+    return KR_OK;
+}
+
+int kr_step_timing_read(double* launch_us, double* span_us, int n, int* n_read) {
+    KR_REQUIRE(n == 0 || (launch_us && span_us), "kr_step_timing_read: null pointer");
+    std::lock_guard<std::mutex> lock(g_step.mu);
+    KR_REQUIRE(g_step.stamps && g_step.n > 0, "kr_step_timing_read: no timed step has run");
+    int dev = 0, khz = 0;
+    KR_HIP(hipGetDevice(&dev));
+    KR_REQUIRE(dev == g_step.dev, "kr_step_timing_read: the timed step ran on device %d",
+               g_step.dev);
+    KR_HIP(hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, dev));
+    KR_REQUIRE(khz > 0, "kr_step_timing_read: no steady-counter rate");
+    KR_HIP(hipDeviceSynchronize());
+    const int k = std::min(n, g_step.n);
+    std::vector<unsigned long long> h;
+    for (int i = 0; i < k; i++) {
+        const size_t used = 2ull * KR_STAMP_WAVES * g_step.grid[i];
+        h.resize(used);
+        KR_HIP(hipMemcpy(h.data(), g_step.stamps + (size_t)i * kStampLayerU64, used * 8,
+                         hipMemcpyDeviceToHost));
+        unsigned long long t0 = ~0ull, t1 = 0;
+        for (size_t j = 0; j < used; j += 2) {
+            if (!h[j]) continue;
+            t0 = std::min(t0, h[j]);
+            t1 = std::max(t1, h[j + 1]);
+        }
+        KR_REQUIRE(t1 > 0, "kr_step_timing_read: layer %d has no stamps", i);
+        span_us[i] = (double)(t1 - t0) * 1000.0 / khz;
+        launch_us[i] = -1.0;
+        if (g_step.eager) {
+            float ms = 0.f;
+            KR_HIP(hipEventElapsedTime(&ms, g_step.ev[i][0], g_step.ev[i][1]));
+            launch_us[i] = 1000.0 * ms;
+        }
+    }
+    if (n_read) *n_read = k;
+    g_step.n = 0;
     return KR_OK;
 }
 
