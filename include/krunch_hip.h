@@ -322,6 +322,7 @@ int kr_reset_phase_times(void);
  * (n_read = min(n, layers)), the launch's event duration (-1 for a graph
  * step) and its wave span (last wave end minus first wave start), in
  * microseconds; it fails if no timed step ran since the last reading. */
+int kr_step_timing(int phase, int* previous);
 int kr_step_timing_read(double* launch_us, double* span_us, int n, int* n_read);
 
 /* replaces launch_krunch_wkv_forward (wkv_kernel.cu:75-92), fused with the
