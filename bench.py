@@ -61,7 +61,8 @@ def parse():
     ap.add_argument("--kernel-probe", action="store_true",
                     help="only run a 256 MiB device copy (counter calibration), 8 launches of "
                          "the dominant kernel and 2 eager launches of each other hot kernel at "
-                         "the bench shapes, for rocprofv3 --pmc runs")
+                         "the bench shapes (the packed products and head included), for "
+                         "rocprofv3 --pmc runs")
     return ap.parse_args()
 
 
@@ -138,6 +139,23 @@ def kernel_probe(weights16, B):
                   res.data_ptr(), gate.data_ptr(), s)
     torch.cuda.synchronize()
     del A, res, gate, out
+    # packed channel-mix key product (K = 768, N = 3072, relu^2) at the window shape
+    A = torch.rand((Mp, N), device=dev).half()
+    out = torch.empty((Mp, K), dtype=torch.float16, device=dev)
+    for _ in range(2):
+        _lib.call("kr_det_matmul", A.data_ptr(), Mp, N, P.tensors["0.fKt"].data_ptr(), N, K,
+                  out.data_ptr(), K, 3, None, None, s)
+    torch.cuda.synchronize()
+    del A, out
+    # the compress head: LN_out + the 768 x 50277 product on one 4096-row block
+    xh = torch.randn((4096, P.C), device=dev).half()
+    xnh = torch.empty((4096, P.C), dtype=torch.float16, device=dev)
+    lh = torch.empty((4096, cpp_path.logits_ld(P.V)), dtype=torch.float16, device=dev)
+    for _ in range(2):
+        _lib.call("kr_head_logits", P.ptr, xh.data_ptr(), 4096, xnh.data_ptr(), lh.data_ptr(),
+                  cpp_path.logits_ld(P.V), s)
+    torch.cuda.synchronize()
+    del xh, xnh, lh
     # packed WKV over a 1024-token window of B streams
     k = torch.randn((B, 1024, P.C), device=dev)
     v = torch.randn((B, 1024, P.C), device=dev)

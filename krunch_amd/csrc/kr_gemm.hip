@@ -246,8 +246,11 @@ __global__ void __launch_bounds__(256, 2) gemm_tile_kernel(kr_gemm_args g) {
 // consecutive columns of one row (vector stores); every output element is
 // still the 8-deep chain per 256-wide slice folded in order, the bits of the
 // other kernels.
-constexpr int kBigM = 256, kBigN = 128;
-constexpr int kBigStage = (kBigM + kBigN) * 8;   // 16-byte units per stage (48 KB)
+// Tile shapes BM x BN of the persistent kernel: 256 x 128 (4 x 2 waves) or
+// 128 x 256 (2 x 4 waves); either way a stage holds BM + BN = 384 rows of a
+// 64-wide K step (48 KB) and every wave owns a 64 x 64 output block.
+constexpr int kBigRows = 384;
+constexpr int kBigStage = kBigRows * 8;          // 16-byte units per stage (48 KB)
 
 __device__ __forceinline__ int big_pos(int r, int kc) {
     return 64 * (r >> 3) + 8 * (r & 7) + (kc ^ ((r >> 1) & 7));
@@ -296,9 +299,11 @@ __device__ __forceinline__ void store_row4(const kr_gemm_args& g, int m, int n, 
 
 // Tile t of the launch (the dealing of tile_of, for a launch of `grid`
 // virtual blocks, in groups of group_m row tiles): false past the last tile.
+template <int BM>
 __device__ __forceinline__ bool big_tile(const kr_gemm_args& g, int vb, int group_m, int& m_t,
                                          int& n_t) {
-    const int gy = (g.M + kBigM - 1) / kBigM, gx = (g.N + kBigN - 1) / kBigN;
+    constexpr int BN = kBigRows - BM;
+    const int gy = (g.M + BM - 1) / BM, gx = (g.N + BN - 1) / BN;
     const int T = gx * gy, per = (T + 7) / 8;
     const int t = (vb & 7) * per + (vb >> 3);
     if (t >= T || (vb >> 3) >= per) return false;
@@ -319,8 +324,8 @@ __device__ __forceinline__ bool big_tile(const kr_gemm_args& g, int vb, int grou
 // the channel-mix value product at K = 3072 is fastest with 1; the fp16
 // compress window takes 118.5-118.9 ms against 120.1-120.7 at 8 (A B A B
 // on one box, same bits), w8a8 compress +1.1%.
-int big_group_m(int K, bool i8) {
-    const long long panel = (long long)kBigM * K * (i8 ? 1 : 2);
+int big_group_m(int K, bool i8, int BM) {
+    const long long panel = (long long)BM * K * (i8 ? 1 : 2);
     const long long g = (2ll << 20) / panel;
     return (int)std::min<long long>(8, std::max<long long>(1, g));
 }
@@ -332,18 +337,20 @@ int big_group_m(int K, bool i8) {
 // I8: int8 operands (w8a8), moved as 16-bit pairs: a 64-half K step is 128
 // int8 k and each 32-half block one v_mfma_i32_16x16x64_i8; the int32 sum is
 // exact (no slices), dequantised once per output: (float(acc) * sa[m]) * sw[n].
-template <int EP, bool I8>
+template <int EP, bool I8, int BM>
 __global__ void __launch_bounds__(512, 1) gemm_big_kernel(kr_gemm_args g, int n_virtual, int group_m) {
+    constexpr int BN = kBigRows - BM, WN = BN / 64, AU = BM / 8;   // AU: copy units of A
+    static_assert(BM == 256 || BM == 128, "tile shape");
     __shared__ __attribute__((aligned(1024))) kr_half8 ring[3 * kBigStage];   // 3 x 48 KB
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wm = wave >> 1, wn = wave & 1;
+    const int wm = wave / WN, wn = wave % WN;
     const int G = gridDim.x;
     const int KS = (I8 ? g.K >> 1 : g.K) / 64;    // 64-half K steps (fp16: K % 256 == 0)
     const long long lda16 = I8 ? g.lda >> 1 : g.lda, ldw16 = I8 ? g.ldw >> 1 : g.ldw;
 
-    // Copy instruction u = 6 wave + i of a stage: u < 32 fills A rows 8u..8u+7,
-    // u >= 32 fills W rows 8(u-32).. (rows past M or N repeat the last one;
+    // Copy instruction u = 6 wave + i of a stage: u < AU fills A rows 8u..8u+7,
+    // u >= AU fills W rows 8(u-AU).. (rows past M or N repeat the last one;
     // their outputs are never stored). Lane l moves chunk (row 8u' + l/8,
     // kc = (l % 8) ^ ((row / 2) % 8)).
     const unsigned ring_base = (unsigned)(uintptr_t)(__attribute__((address_space(3))) char*)ring;
@@ -352,14 +359,14 @@ __global__ void __launch_bounds__(512, 1) gemm_big_kernel(kr_gemm_args g, int n_
     #pragma unroll
     for (int i = 0; i < 6; i++) {
         const int u = wave * 6 + i;
-        crow[i] = 8 * (u < 32 ? u : u - 32) + (lane >> 3);
+        crow[i] = 8 * (u < AU ? u : u - AU) + (lane >> 3);
         ckc[i] = (lane & 7) ^ ((crow[i] >> 1) & 7);
         dst[i] = ring_base + (unsigned)(u * 1024);
     }
     auto sources = [&](int m0, int n0, const char* (&src)[6]) {
         #pragma unroll
         for (int i = 0; i < 6; i++) {
-            if (wave * 6 + i < 32)
+            if (wave * 6 + i < AU)
                 src[i] = reinterpret_cast<const char*>(g.A + (size_t)min(m0 + crow[i], g.M - 1) * lda16 + ckc[i] * 8);
             else
                 src[i] = reinterpret_cast<const char*>(g.Wt + (size_t)min(n0 + crow[i], g.N - 1) * ldw16 + ckc[i] * 8);
@@ -373,10 +380,10 @@ __global__ void __launch_bounds__(512, 1) gemm_big_kernel(kr_gemm_args g, int n_
     };
 
     int vb = blockIdx.x, m_t, n_t;
-    if (!big_tile(g, vb, group_m, m_t, n_t)) return;
+    if (!big_tile<BM>(g, vb, group_m, m_t, n_t)) return;
     const char* src[6];
     const char* nsrc[6];
-    sources(m_t * kBigM, n_t * kBigN, src);
+    sources(m_t * BM, n_t * BN, src);
     int q = 0;                                     // running step number
     issue(src, 0, 0);
     issue(src, 1, 1);
@@ -386,10 +393,10 @@ __global__ void __launch_bounds__(512, 1) gemm_big_kernel(kr_gemm_args g, int n_
                         ((EP != KR_EP_RESID && EP != KR_EP_GATED) || ((uintptr_t)g.res & 7) == 0) &&
                         (EP != KR_EP_GATED || ((uintptr_t)g.gate & 7) == 0);
     while (true) {
-        const int m0 = m_t * kBigM, n0 = n_t * kBigN;
+        const int m0 = m_t * BM, n0 = n_t * BN;
         int nm_t = 0, nn_t = 0;
-        const bool has_next = vb + G < n_virtual && big_tile(g, vb + G, group_m, nm_t, nn_t);
-        if (has_next) sources(nm_t * kBigM, nn_t * kBigN, nsrc);
+        const bool has_next = vb + G < n_virtual && big_tile<BM>(g, vb + G, group_m, nm_t, nn_t);
+        if (has_next) sources(nm_t * BM, nn_t * BN, nsrc);
         typedef typename std::conditional<I8, kr_int4, kr_float4>::type Acc;
         Acc acc[4][4];
         kr_float4 tot[4][4];
@@ -409,7 +416,7 @@ __global__ void __launch_bounds__(512, 1) gemm_big_kernel(kr_gemm_args g, int n_
             if (ks + 2 < KS) issue(src, ks + 2, q + 2);
             else if (has_next) issue(nsrc, ks + 2 - KS, q + 2);
             const kr_half8* As = ring + (q % 3) * kBigStage;
-            const kr_half8* Ws = As + kBigM * 8;
+            const kr_half8* Ws = As + BM * 8;
             if (!I8 && (ks & 3) == 0) {
                 #pragma unroll
                 for (int i = 0; i < 4; i++)
@@ -460,7 +467,7 @@ __global__ void __launch_bounds__(512, 1) gemm_big_kernel(kr_gemm_args g, int n_
             }
         }
         // lane: row 64 wm + 16 i + lane % 16, columns 64 wn + 16 t + 4 (lane / 16) .. + 3
-        const bool full_m = m0 + kBigM <= g.M;
+        const bool full_m = m0 + BM <= g.M;
         #pragma unroll
         for (int i = 0; i < 4; i++) {
             const int m = m0 + 64 * wm + 16 * i + lr;
@@ -480,23 +487,42 @@ __global__ void __launch_bounds__(512, 1) gemm_big_kernel(kr_gemm_args g, int n_
     }
 }
 
-template <bool I8>
-int launch_big(const kr_gemm_args& g, int ep, hipStream_t s) {
-    const long long T = (long long)((g.N + kBigN - 1) / kBigN) * ((g.M + kBigM - 1) / kBigM);
+template <bool I8, int BM>
+int launch_big_bm(const kr_gemm_args& g, int ep, hipStream_t s) {
+    constexpr int BN = kBigRows - BM;
+    const long long T = (long long)((g.N + BN - 1) / BN) * ((g.M + BM - 1) / BM);
     const int n_virtual = (int)((T + 7) / 8 * 8);
     const int grid = n_virtual < 256 ? n_virtual : 256;   // one workgroup per CU
-    const int gm = big_group_m(g.K, I8);
+    const int gm = big_group_m(g.K, I8, BM);
     switch (ep) {
-        case KR_EP_F32: gemm_big_kernel<KR_EP_F32, I8><<<grid, 512, 0, s>>>(g, n_virtual, gm); break;
-        case KR_EP_F16: gemm_big_kernel<KR_EP_F16, I8><<<grid, 512, 0, s>>>(g, n_virtual, gm); break;
-        case KR_EP_SIGMOID: gemm_big_kernel<KR_EP_SIGMOID, I8><<<grid, 512, 0, s>>>(g, n_virtual, gm); break;
-        case KR_EP_RELUSQ: gemm_big_kernel<KR_EP_RELUSQ, I8><<<grid, 512, 0, s>>>(g, n_virtual, gm); break;
-        case KR_EP_RESID: gemm_big_kernel<KR_EP_RESID, I8><<<grid, 512, 0, s>>>(g, n_virtual, gm); break;
-        case KR_EP_GATED: gemm_big_kernel<KR_EP_GATED, I8><<<grid, 512, 0, s>>>(g, n_virtual, gm); break;
+        case KR_EP_F32: gemm_big_kernel<KR_EP_F32, I8, BM><<<grid, 512, 0, s>>>(g, n_virtual, gm); break;
+        case KR_EP_F16: gemm_big_kernel<KR_EP_F16, I8, BM><<<grid, 512, 0, s>>>(g, n_virtual, gm); break;
+        case KR_EP_SIGMOID: gemm_big_kernel<KR_EP_SIGMOID, I8, BM><<<grid, 512, 0, s>>>(g, n_virtual, gm); break;
+        case KR_EP_RELUSQ: gemm_big_kernel<KR_EP_RELUSQ, I8, BM><<<grid, 512, 0, s>>>(g, n_virtual, gm); break;
+        case KR_EP_RESID: gemm_big_kernel<KR_EP_RESID, I8, BM><<<grid, 512, 0, s>>>(g, n_virtual, gm); break;
+        case KR_EP_GATED: gemm_big_kernel<KR_EP_GATED, I8, BM><<<grid, 512, 0, s>>>(g, n_virtual, gm); break;
         default: return kr_fail(KR_EINVAL, "unknown epilogue %d", ep);
     }
     KR_LAUNCHED();
     return KR_OK;
+}
+
+// Tile shape: both shapes copy the same bytes per MAC (M N K (1/BM + 1/BN));
+// they differ in which operand is re-read. The layer products of a compress
+// window (M = B T >> N) re-read A, hundreds of MB that stream from HBM, once
+// per BN columns: 128 x 256 tiles halve that. The head (N = V >> M rows per
+// block) re-reads W, 77 MB, once per BM rows: it keeps 256 x 128. Measured
+// on MI355X (A B A B, one box): fp16 compress 8,575 / 8,520 KB/s with
+// 256 x 128 everywhere against 8,576 / 8,570 with this rule, w8a8 compress
+// 9,755 / 9,747 against 9,849 / 9,856 (same bits: one reduction contract).
+int big_tile_rows(const kr_gemm_args& g) {
+    return (long long)g.M >= 4ll * g.N && g.N >= 256 ? 128 : 256;
+}
+
+template <bool I8>
+int launch_big(const kr_gemm_args& g, int ep, hipStream_t s) {
+    return big_tile_rows(g) == 128 ? launch_big_bm<I8, 128>(g, ep, s)
+                                   : launch_big_bm<I8, 256>(g, ep, s);
 }
 
 // ---------------------------------------------------------------------------
