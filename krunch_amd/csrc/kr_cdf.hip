@@ -540,11 +540,25 @@ __device__ __forceinline__ void cdf_row(const void* __restrict__ input, long lon
     int32_t* orow = nullptr;
     if constexpr (MODE == M_CDF || MODE == M_COUNTS)
         orow = reinterpret_cast<int32_t*>(out) + (size_t)row * (size_t)out_ld;
+    // A lane only notes, per register slice, whether any of its slots holds
+    // p == pmax (one compare per element, the flags kept as lane masks); the
+    // lanes that do (a few per row) find their lowest such slot afterwards,
+    // in the lowest flagged slice only.
+    bool any_hit[kMaxIt];
+    auto is_hit = [&](int it, int k, float p) {
+        bool hit = p == pmax;
+        if constexpr (IN == IN_PROBS_F32) {
+            const int nf = leaf_full(len[it]), rm = leaf_rem(len[it]);
+            hit = hit && (k < 16 ? (k < nf) : (j < rm));
+        }
+        return hit;
+    };
     #pragma unroll
     for (int it = kMaxIt - 1; it >= 0; it--) {
         const int nf = leaf_full(len[it]), rm = leaf_rem(len[it]);
         int ls = 0;
         lsum[it] = 0;
+        any_hit[it] = false;
         if (!act[it]) continue;
         #pragma unroll
         for (int k = 16; k >= 0; k--) {
@@ -552,16 +566,27 @@ __device__ __forceinline__ void cdf_row(const void* __restrict__ input, long lon
             const float p = div_by(v[it][k], denom, rdenom);
             const int f = scaled_floor<IN>(p, scale);
             ls += f;
-            bool hit = p == pmax;
-            if constexpr (IN == IN_PROBS_F32 || MODE == M_CDF || MODE == M_COUNTS) {
+            if constexpr (MODE == M_CDF || MODE == M_COUNTS) {
                 const bool live = k < 16 ? (k < nf) : (j < rm);
-                if constexpr (IN == IN_PROBS_F32) hit = hit && live;
-                if constexpr (MODE == M_CDF || MODE == M_COUNTS)
-                    if (live) orow[slot_index(start[it], len[it], j, k) + 1] = f + 1;
+                if (live) orow[slot_index(start[it], len[it], j, k) + 1] = f + 1;
             }
-            if (hit) bslot = 32 * it + k;
+            any_hit[it] = any_hit[it] || is_hit(it, k, p);
         }
         lsum[it] = ls + nf + (j < rm ? 1 : 0);
+    }
+    // a lane's lowest indices are in its lowest slice: the first flagged
+    // slice holds its first maximum; slots from the highest index down, the
+    // last hit kept
+    #pragma unroll
+    for (int it = 0; it < kMaxIt; it++) {
+        const bool first = any_hit[it] && bslot < 0;
+        if (first) {
+            #pragma unroll
+            for (int k = 16; k >= 0; k--) {
+                if (k == 16 && !tail[it]) continue;
+                if (is_hit(it, k, div_by(v[it][k], denom, rdenom))) bslot = 32 * it + k;
+            }
+        }
     }
     int key = 0x7fffffff;                 // (index << 9) | leaf of that maximum
     if (bslot >= 0) {

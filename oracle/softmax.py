@@ -12,8 +12,8 @@ fixes every rounding so that CPU and GPU agree bit for bit:
   q_i = e_i * (1 / S)           # one IEEE division per row
   cdf = probs_to_cdf(q)         # cdf.py:22-74, bit for bit
 
-`kexp` is a Cody-Waite reduction x = n*ln2 + r, |r| <= ln2/2, followed by the
-degree-7 Taylor polynomial of e^r in Horner form, then scaling by 2^n. The
+`kexp` is a Cody-Waite reduction x = n*ln2 + r, |r| <= ln2/2, followed by a
+degree-6 minimax polynomial of e^r in Horner form, then scaling by 2^n. The
 reduction and every Horner step are fused multiply-adds (one rounding each);
 the multiply by log2(e) and the round to integer are single IEEE operations.
 numpy has no float32 FMA, so kexp is computed by the C restatement in

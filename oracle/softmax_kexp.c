@@ -6,7 +6,9 @@
  *   xc = max(x, -87.5)                 (NaN and -inf -> -87.5)
  *   n  = rint(xc * log2(e))            (round half to even)
  *   r  = fma(-n, ln2_lo, fma(-n, ln2_hi, xc))
- *   p  = Horner by fma of the degree-7 Taylor polynomial of e^r
+ *   p  = Horner by fma of a degree-6 polynomial of e^r: a minimax fit on
+ *        [-ln2/2, ln2/2] for relative error (c0 = c1 = 1; c2..c6 rounded to
+ *        float32 one at a time, lowest order first, the rest refitted)
  *   e  = ldexp(p, n)                   (exact: the result is normal)
  *   kexp(x) = e if x >= -87 else 0
  *
@@ -24,19 +26,18 @@ static float kexp1(float x) {
     const float log2e = f32_bits(0x3FB8AA3Bu);
     const float ln2_hi = f32_bits(0x3F317200u);
     const float ln2_lo = f32_bits(0x35BFBE8Eu);
-    const float c7 = f32_bits(0x39500D01u), c6 = f32_bits(0x3AB60B61u),
-                c5 = f32_bits(0x3C088889u), c4 = f32_bits(0x3D2AAAABu),
-                c3 = f32_bits(0x3E2AAAABu);
+    const float c6 = f32_bits(0x3AB51E82u), c5 = f32_bits(0x3C091C2Bu),
+                c4 = f32_bits(0x3D2AAC5Fu), c3 = f32_bits(0x3E2AAA4Au),
+                c2 = f32_bits(0x3EFFFFFEu);
     const float xc = fmaxf(x, -87.5f);
     const float n = rintf(xc * log2e);
     float r = fmaf(-n, ln2_hi, xc);
     r = fmaf(-n, ln2_lo, r);
-    float p = c7;
-    p = fmaf(p, r, c6);
+    float p = c6;
     p = fmaf(p, r, c5);
     p = fmaf(p, r, c4);
     p = fmaf(p, r, c3);
-    p = fmaf(p, r, 0.5f);
+    p = fmaf(p, r, c2);
     p = fmaf(p, r, 1.0f);
     p = fmaf(p, r, 1.0f);
     const float e = ldexpf(p, (int)n);

@@ -12,9 +12,12 @@ def _ulp_err(got, ref):
 
 
 def test_kexp_accuracy_dense_grid():
+    """Faithful on a dense grid: the degree-6 minimax polynomial is within
+    0.053 ulp of e^r in exact arithmetic; with the float32 roundings of the
+    reduction and the Horner steps the result stays below 1 ulp (0.87 max)."""
     x = np.linspace(-86.99, 0.0, 2_000_001, dtype=np.float32)
     got = osm.kexp(x)
-    assert _ulp_err(got, np.exp(x.astype(np.float64))).max() <= 2.0
+    assert _ulp_err(got, np.exp(x.astype(np.float64))).max() < 1.0
     assert (np.diff(got.astype(np.float64)) >= 0).all()          # monotone
 
 
