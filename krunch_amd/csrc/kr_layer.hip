@@ -158,14 +158,21 @@ struct WkvState {
 };
 
 // One token of the recurrence; returns ry.
-// DET: exps by kr_kexp (the w8a8 codec; every argument here is <= 0).
+// DET: exps by kr_kexp and an IEEE division (the w8a8 codec, which the oracle
+// restates bit for bit; every exp argument here is <= 0). Otherwise (the fp16
+// codec) the hardware exp and the quotient as numerator times the hardware
+// reciprocal (~1 ulp; y is rounded to fp16 next): the packed and stepped
+// paths both run this function, so their bits agree.
 template <bool DET>
 __device__ __forceinline__ kr_half wkv_token(WkvState& st, float w, float u, float kk, float vv,
                                              float rr) {
     const float ww = u + kk;
     const float p1 = fmaxf(st.p, ww);
     const float e1 = kr_exp_t<DET>(st.p - p1), e2 = kr_exp_t<DET>(ww - p1);
-    const float y = (e1 * st.a + e2 * vv) / (e1 * st.b + e2);
+    const float num = e1 * st.a + e2 * vv, den = e1 * st.b + e2;   // den >= min(1, bb) > 0
+    float y;
+    if constexpr (DET) y = num / den;
+    else y = num * __builtin_amdgcn_rcpf(den);
     const kr_half ry = kr_f16(rr * (float)kr_f16(y));
     const float ww2 = w + st.p;
     const float p2 = fmaxf(ww2, kk);
