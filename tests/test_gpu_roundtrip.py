@@ -251,3 +251,34 @@ def test_graph_decode_leaves_the_eager_state(eng, eng_w8a8, codec):
         got = _decode_direct(eng, enc, splits, use_graph=True)
         for name, a, g in zip(("tokens", "count", "coder", "syms", "model state"), ref, got):
             assert torch.equal(a, g), f"{name} differs after calls of {splits} steps"
+
+
+@pytest.mark.parametrize("graph,phase", [(True, 5), (False, 6), (True, 3)])
+def test_step_timing_changes_nothing_and_reports_each_layer(eng, graph, phase):
+    """kr_step_timing: the timed product of every layer stores its waves'
+    start and end (and, eagerly launched, takes dispatch events); decoding
+    with it on gives the bits of decoding with it off, and it reports one
+    positive duration per layer (no event duration for a graph step)."""
+    import ctypes
+    from krunch_amd import _lib
+    toks = [synthetic.zipf_tokens(1, n, seed_base=4700 + i)[0] for i, n in enumerate([25, 8, 19])]
+    enc = eng.compress_tokens_batched(toks)
+    ref = _decode_direct(eng, enc, [25], use_graph=graph)
+    L = _lib.lib()
+    _lib.call("kr_step_timing", phase, None)
+    try:
+        got = _decode_direct(eng, enc, [25], use_graph=graph)
+        launch, span = (ctypes.c_double * 64)(), (ctypes.c_double * 64)()
+        n = ctypes.c_int(0)
+        _lib.call("kr_step_timing_read", launch, span, 64, ctypes.byref(n))
+    finally:
+        L.kr_step_timing(-1, None)
+    for name, a, g in zip(("tokens", "count", "coder", "syms", "model state"), ref, got):
+        assert torch.equal(a, g), f"{name} differs with the step timing on"
+    assert n.value == 12
+    for i in range(12):
+        assert 0.0 < span[i] < 1000.0, (i, span[i])
+        if graph:
+            assert launch[i] == -1.0
+        else:
+            assert 0.0 < launch[i] < 1000.0, (i, launch[i])
