@@ -42,7 +42,7 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-decode-steps", type=int, default=1024,
                     help="CPU baseline: tokens decoded (all of the window by default)")
-    ap.add_argument("--head-rows", type=int, default=4096,
+    ap.add_argument("--head-rows", type=int, default=8192,
                     help="compress: rows per head GEMM + CDF block (the logits buffer holds this many rows)")
     ap.add_argument("--groups", type=int, default=1,
                     help="decode the B streams as this many concurrent groups (graph branches)")

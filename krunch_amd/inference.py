@@ -44,9 +44,10 @@ CDF_PRECISION = 24
 DEFAULT_STREAM_BATCH = cpp_path.DEFAULT_STREAM_BATCH
 
 # Rows per head GEMM + CDF block of a compress window: the logits buffer
-# holds this many rows (4096 x 50280 fp16 = 412 MB); 4096-row blocks keep the
-# head on the persistent 256x128 GEMM kernel.
-HEAD_ROWS = 4096
+# holds this many rows (8192 x 50280 fp16 = 824 MB of the 288 GB). Measured on
+# MI355X (bench window, A B A B): compress 8,804 / 8,793 KB/s at 4,096 rows,
+# 8,838 / 8,833 at 8,192, 8,748 / 8,680 at 16,384.
+HEAD_ROWS = 8192
 
 # Largest coder buffer of one lockstep call, in bytes. Stream offsets into it
 # are int32 and its length is a uint32 in the C ABI (the reference's

@@ -2,7 +2,7 @@
 
 The compress window of a real config runs kernels no toy-shape test reaches:
 the persistent 256x128 GEMM with its vectorised epilogues (M = B*T >= 4096),
-the packed WKV over T = 1024, the head and CDF in 4096-row blocks. These tests
+the packed WKV over T = 1024, the head and CDF in 8192-row blocks. These tests
 check them where exactness is defined:
   * logits of sampled streams within 1e-2 max-abs of the fp32 oracle
     (rows are batch-invariant, so the oracle runs on those streams alone);
