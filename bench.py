@@ -66,7 +66,7 @@ def parse():
     return ap.parse_args()
 
 
-def kernel_probe(weights16, B):
+def kernel_probe(weights16, B, head_rows):
     """A plain copy of known size, then the dominant kernel, eagerly (one
     dispatch each), so hardware counters can be read per dispatch."""
     import ctypes
@@ -147,12 +147,12 @@ def kernel_probe(weights16, B):
                   out.data_ptr(), K, 3, None, None, s)
     torch.cuda.synchronize()
     del A, out
-    # the compress head: LN_out + the 768 x 50277 product on one 4096-row block
-    xh = torch.randn((4096, P.C), device=dev).half()
-    xnh = torch.empty((4096, P.C), dtype=torch.float16, device=dev)
-    lh = torch.empty((4096, cpp_path.logits_ld(P.V)), dtype=torch.float16, device=dev)
+    # the compress head: LN_out + the 768 x 50277 product on one block of head_rows rows
+    xh = torch.randn((head_rows, P.C), device=dev).half()
+    xnh = torch.empty((head_rows, P.C), dtype=torch.float16, device=dev)
+    lh = torch.empty((head_rows, cpp_path.logits_ld(P.V)), dtype=torch.float16, device=dev)
     for _ in range(2):
-        _lib.call("kr_head_logits", P.ptr, xh.data_ptr(), 4096, xnh.data_ptr(), lh.data_ptr(),
+        _lib.call("kr_head_logits", P.ptr, xh.data_ptr(), head_rows, xnh.data_ptr(), lh.data_ptr(),
                   cpp_path.logits_ld(P.V), s)
     torch.cuda.synchronize()
     del xh, xnh, lh
@@ -171,8 +171,8 @@ def kernel_probe(weights16, B):
                   r.data_ptr(), aa.data_ptr(), bb.data_ptr(), pp.data_ptr(), ry.data_ptr(), s)
     torch.cuda.synchronize()
     del k, v, r, ry
-    # softmax -> CDF -> symbol interval for 4096 rows of logits (the compress CDF stage)
-    rows = 4096
+    # softmax -> CDF -> symbol interval for head_rows rows of logits (the compress CDF stage)
+    rows = head_rows
     ld = cpp_path.logits_ld(P.V)
     logits = (torch.randn((rows, ld), device=dev) * 3).half()
     syms = torch.randint(0, P.V, (rows,), device=dev, dtype=torch.int32)
@@ -707,7 +707,7 @@ def main():
     from krunch_amd import synthetic
     weights16 = synthetic.make_weights()
     if args.kernel_probe:
-        kernel_probe(weights16, args.batch)
+        kernel_probe(weights16, args.batch, args.head_rows)
         return
     r = gpu_bench(args, weights16, step_probe=True)
     t = r["t_c"] + r["t_d"]
