@@ -133,13 +133,26 @@ int kr_gemm_panel_ns(const kr_gemm_args* jobs, int njobs);
 int kr_gemm_launch_multi(const kr_gemm_args* jobs, const int* epilogues, int njobs,
                          hipStream_t stream);
 
+// The head (logits = fp16(LN_out(x) @ head)) has a reduction contract of
+// its own, which the two head kernels below share and no other product uses:
+//   acc = chain of v_mfma_f32_16x16x32_f16 over k = 0, 32, ..., K - 32 from
+//         zero (one chain, no slice partials), out = fp16(acc).
+// A row's logits are therefore the same bits for any M and either kernel.
+// The decode head holds the whole K of its rows in one wave, so one chain
+// costs it nothing; the large-M head gains a 256 x 256 tile from the
+// registers the slice partials would take.
+
 // out[M, N] (row stride ldo) = fp16(A @ W) for the small-M head (M <= 256,
 // K in {256, 512, 768}): A fragment-packed [M rows padded to 16, K], W^T
-// fragment-packed [N padded to 16, K]. Same contract and bits as
-// kr_gemm_launch with KR_EP_F16.
+// fragment-packed [N padded to 16, K].
 bool kr_gemm_head_small_ok(int M, int N, int K);
 int kr_gemm_head_small(const kr_half* Af, const kr_half* Wf, int M, int N, int K, kr_half* out,
                        long long ldo, hipStream_t stream);
+// The same product for any M: A [M, K] row-major (row stride lda), W^T [N, K]
+// row-major (row stride ldw); K % 64 == 0, lda and ldw multiples of 8,
+// A and Wt 16-byte aligned, N * ldw * 2 < 2^31.
+int kr_gemm_head_big(const kr_half* A, long long lda, const kr_half* Wt, long long ldw, int M,
+                     int N, int K, kr_half* out, long long ldo, hipStream_t stream);
 
 
 // Per-row symmetric int8 quantisation of an fp16 [M, K] matrix (kr_quant.hip).

@@ -1253,9 +1253,11 @@ int kr_impl_embed(const kr_model_weights* m, const int32_t* ids, int M, void* x,
 }
 
 // logits[M, ld] = fp16(LN_out(x) @ head); xn is an [M, C] fp16 scratch.
-// Up to 256 rows (the decode step) with a fragment-packed head: LN_out writes
-// xn fragment-packed and the small-M head kernel reads it (same bits). That
-// needs xn to hold M rounded up to 16 rows (xn_rows16).
+// Up to 512 rows (the decode step) with a fragment-packed head: LN_out writes
+// xn fragment-packed and the small-M head kernel reads it. That needs xn to
+// hold M rounded up to 16 rows (xn_rows16). Otherwise xn is row-major and the
+// large-M head kernel runs. Both kernels follow the head's one-chain
+// contract (kr_gemm.h), so a row's logits do not depend on the path.
 int kr_impl_head(const kr_model_weights* m, const void* x, int M, void* xn, void* logits,
                  long long ld, hipStream_t s, bool xn_rows16) {
     if (M == 0) return KR_OK;
@@ -1283,19 +1285,7 @@ int kr_impl_head(const kr_model_weights* m, const void* x, int M, void* xn, void
                                       Hm(logits) + (size_t)r0 * (size_t)ld, ld, s));
         return KR_OK;
     }
-    kr_gemm_args g{};
-    g.A = H(xn);
-    g.lda = m->C;
-    g.Wt = H(m->headT);
-    g.ldw = m->C;
-    g.out = logits;
-    g.ldo = ld;
-    g.res = nullptr;
-    g.gate = nullptr;
-    g.M = M;
-    g.N = m->V;
-    g.K = m->C;
-    return kr_gemm_launch(g, KR_EP_F16, s);
+    return kr_gemm_head_big(H(xn), m->C, H(m->headT), m->C, M, m->V, m->C, Hm(logits), ld, s);
 }
 
 size_t kr_impl_work_bytes(long long M, int C, int F) { return work_bytes(M, C, F); }

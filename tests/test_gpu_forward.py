@@ -157,9 +157,10 @@ def test_pack_fragments_layout():
 @pytest.mark.parametrize("M", [16, 48, 256, 400, 512])
 def test_small_head_equals_tiled_head(model, M):
     """The decode head (A held in registers, fragment-packed weights streamed
-    once; 256-row launches up to 512 rows) gives the 256x128 persistent
-    kernel's logits bit for bit, including the 5-column tail block of
-    V = 50277 and a padded row stride."""
+    once; 256-row launches up to 512 rows) gives the large-M head kernel's
+    logits (256 x 256 tiles, row-major operands) bit for bit: the head's
+    one-chain contract. Includes the 5-column tail block of V = 50277 and a
+    padded row stride."""
     from krunch_amd import _lib
     import ctypes
     _, W = model
@@ -180,3 +181,34 @@ def test_small_head_equals_tiled_head(model, M):
     ref = torch.nn.functional.layer_norm(x.float(), (P.C,), eps=1e-5) @ \
         P.tensors["headT"].float().t()
     assert (outs[0][:, :P.V].float() - ref).abs().max() < 2e-2
+
+
+@pytest.mark.parametrize("M", [1000, 4096 + 37])
+def test_large_m_head_rows_equal_decode_head_rows(model, M):
+    """A row's logits are the same bits whichever head kernel computes it and
+    however many rows share the call: the large-M head at M rows (ragged last
+    row tile, 5-column tail) against the decode head on 256-row slices of the
+    same rows (first, middle and last)."""
+    from krunch_amd import _lib
+    import ctypes
+    _, W = model
+    P = W["prepared"]
+    m_row, _keep = _row_major_only(P)      # no fragment-packed head: the large-M kernel
+    g = torch.Generator(device="cpu").manual_seed(M)
+    x = torch.randn((M, P.C), generator=g).half().cuda()
+    ld = cpp_path.logits_ld(P.V)
+    xn = torch.empty((M, P.C), dtype=torch.float16, device="cuda")
+    big = torch.full((M, ld), float("nan"), dtype=torch.float16, device="cuda")
+    _lib.call("kr_head_logits", ctypes.byref(m_row), x.data_ptr(), M, xn.data_ptr(),
+              big.data_ptr(), ld, _lib.stream_ptr())
+    for r0 in (0, M // 2 - 128, M - 256):
+        xs = x[r0:r0 + 256].contiguous()
+        xns = torch.empty((256, P.C), dtype=torch.float16, device="cuda")
+        small = torch.full((256, ld), float("nan"), dtype=torch.float16, device="cuda")
+        _lib.call("kr_head_logits", P.ptr, xs.data_ptr(), 256, xns.data_ptr(), small.data_ptr(),
+                  ld, _lib.stream_ptr())
+        assert torch.equal(big[r0:r0 + 256, :P.V], small[:, :P.V]), f"rows {r0}.."
+    assert torch.isnan(big[:, P.V:]).all()           # padding columns untouched
+    ref = torch.nn.functional.layer_norm(x.float(), (P.C,), eps=1e-5) @ \
+        P.tensors["headT"].float().t()
+    assert (big[:, :P.V].float() - ref).abs().max() < 2e-2
