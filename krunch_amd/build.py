@@ -20,7 +20,8 @@ OUT_DIR = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libkrunch_hip.so")
 ARCH = os.environ.get("KRUNCH_OFFLOAD_ARCH", "gfx950")
 
-SOURCES = ["kr_rc.hip", "kr_cdf.hip", "kr_gemm.hip", "kr_quant.hip", "kr_layer.hip", "kr_engine.hip"]
+SOURCES = ["kr_rc.hip", "kr_cdf.hip", "kr_gemm.hip", "kr_quant.hip", "kr_layer.hip", "kr_engine.hip",
+           "kr_wide.hip"]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = [f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-ffp-contract=off",

@@ -153,6 +153,11 @@ int kr_gemm_head_small(const kr_half* Af, const kr_half* Wf, int M, int N, int K
 // A and Wt 16-byte aligned, N * ldw * 2 < 2^31.
 int kr_gemm_head_big(const kr_half* A, long long lda, const kr_half* Wt, long long ldw, int M,
                      int N, int K, kr_half* out, long long ldo, hipStream_t stream);
+// The 256 x 256 persistent kernel (kr_wide.hip) on one product without slice
+// partials: the head (KR_EP_F16, fp16 operands) or any epilogue on int8
+// operands (w8a8, exact int32 sums). Needs K a whole number of 128-byte
+// steps, 16-byte aligned operand rows, and N * (W^T row bytes) < 2^31.
+int kr_gemm_launch_wide(const kr_gemm_args& g, int epilogue, hipStream_t stream);
 
 
 // Per-row symmetric int8 quantisation of an fp16 [M, K] matrix (kr_quant.hip).

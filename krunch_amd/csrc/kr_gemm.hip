@@ -25,6 +25,7 @@
 #include <type_traits>
 
 #include "kr_gemm.h"
+#include "kr_gemm_epilogue.h"
 #include "kr_math.h"
 #include "kr_wave.h"
 #include "krunch_hip.h"
@@ -35,27 +36,6 @@ constexpr int kBK = 64;
 constexpr int kPitch = kBK + 8;
 constexpr int kKS = KR_GEMM_KSPLIT;
 static_assert(kKS % kBK == 0, "split must be a multiple of the LDS K tile");
-
-// DET: the w8a8 codec's sigmoid (kr_sigmoid_k); int8 kernels pass I8.
-template <int EP, bool DET = false>
-__device__ __forceinline__ void store_one(const kr_gemm_args& g, int m, int n, float acc) {
-    const size_t o = (size_t)m * (size_t)g.ldo + (size_t)n;
-    if constexpr (EP == KR_EP_F32) {
-        reinterpret_cast<float*>(g.out)[o] = acc;
-    } else {
-        const float h = (float)kr_f16(acc);
-        float y;
-        if constexpr (EP == KR_EP_F16) y = h;
-        else if constexpr (EP == KR_EP_SIGMOID) y = kr_sigmoid_t<DET>(h);
-        else if constexpr (EP == KR_EP_RELUSQ) { const float r = h > 0.0f ? h : 0.0f; y = r * r; }
-        else if constexpr (EP == KR_EP_RESID) y = (float)g.res[o] + h;
-        else {
-            const float gh = (float)kr_f16((float)g.gate[o] * h);
-            y = (float)g.res[o] + gh;
-        }
-        reinterpret_cast<kr_half*>(g.out)[o] = kr_f16(y);
-    }
-}
 
 __device__ __forceinline__ kr_float4 add4(kr_float4 a, kr_float4 b) {
     return kr_float4{a[0] + b[0], a[1] + b[1], a[2] + b[2], a[3] + b[3]};
@@ -86,7 +66,6 @@ __device__ __forceinline__ bool tile_of(const kr_gemm_args& g, int BM, int BN, i
     n_t = r / gm;
     return true;
 }
-__device__ __forceinline__ kr_int4 as_i4(kr_half8 v) { return __builtin_bit_cast(kr_int4, v); }
 
 // I8: int8 operands moved as 16-bit pairs (a 64-half K tile = 128 int8 k; a
 // 32-half k step = one v_mfma_i32_16x16x64_i8), int32 accumulation.
@@ -252,49 +231,12 @@ __global__ void __launch_bounds__(256, 2) gemm_tile_kernel(kr_gemm_args g) {
 constexpr int kBigRows = 384;
 constexpr int kBigStage = kBigRows * 8;          // 16-byte units per stage (48 KB)
 
-__device__ __forceinline__ int big_pos(int r, int kc) {
-    return 64 * (r >> 3) + 8 * (r & 7) + (kc ^ ((r >> 1) & 7));
-}
 
 // 16-byte asynchronous copy global -> LDS: lane l writes LDS byte address
 // lds + 16 l. Invisible to the compiler's wait-count tracking (see above).
 __device__ __forceinline__ void big_copy(const void* src, unsigned lds) {
     asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off"
                  :: "s"(lds), "v"(src) : "memory", "m0");
-}
-
-// Epilogue of 4 consecutive columns n..n+3 of row m (vec: aligned vector
-// access allowed and all 4 columns < N).
-template <int EP, bool DET>
-__device__ __forceinline__ void store_row4(const kr_gemm_args& g, int m, int n, kr_float4 acc,
-                                           bool vec) {
-    if (!vec) {
-        #pragma unroll
-        for (int r = 0; r < 4; r++)
-            if (n + r < g.N) store_one<EP, DET>(g, m, n + r, acc[r]);
-        return;
-    }
-    const size_t o = (size_t)m * (size_t)g.ldo + (size_t)n;
-    if constexpr (EP == KR_EP_F32) {
-        *reinterpret_cast<kr_float4*>(reinterpret_cast<float*>(g.out) + o) = acc;
-    } else {
-        kr_half4 rv = kr_half4{0, 0, 0, 0}, gv = kr_half4{0, 0, 0, 0};
-        if constexpr (EP == KR_EP_RESID || EP == KR_EP_GATED) rv = *reinterpret_cast<const kr_half4*>(g.res + o);
-        if constexpr (EP == KR_EP_GATED) gv = *reinterpret_cast<const kr_half4*>(g.gate + o);
-        kr_half4 h;
-        #pragma unroll
-        for (int r = 0; r < 4; r++) {
-            const float x = (float)kr_f16(acc[r]);
-            float y;
-            if constexpr (EP == KR_EP_F16) y = x;
-            else if constexpr (EP == KR_EP_SIGMOID) y = kr_sigmoid_t<DET>(x);
-            else if constexpr (EP == KR_EP_RELUSQ) { const float rr = x > 0.0f ? x : 0.0f; y = rr * rr; }
-            else if constexpr (EP == KR_EP_RESID) y = (float)rv[r] + x;
-            else y = (float)rv[r] + (float)kr_f16((float)gv[r] * x);
-            h[r] = kr_f16(y);
-        }
-        *reinterpret_cast<kr_half4*>(reinterpret_cast<kr_half*>(g.out) + o) = h;
-    }
 }
 
 // Tile t of the launch (the dealing of tile_of, for a launch of `grid`
@@ -1282,7 +1224,16 @@ int kr_gemm_launch_multi(const kr_gemm_args* jobs, const int* eps, int njobs, hi
         KR_REQUIRE(g.Wt, "gemm: row-major W missing");
         int rc;
         if (g.i8) {
-            if (g.M >= 4096 && (g.K >> 1) % 64 == 0) rc = launch_big<true>(g, eps[j], s);
+            // the 256 x 256 kernel pays where a tile has many K steps or the
+            // product many column tiles; measured on MI355X at M = 262144:
+            // ffn K (K = 768, N = 3072) -4%, ffn V (K = 3072, N = 768)
+            // -1.5%, the 768 x 768 products +7 to +14% (six K steps per
+            // tile with one in flight)
+            if (g.M >= 4096 && (g.N >= 2048 || g.K >= 2048) && g.K % 128 == 0 &&
+                g.lda % 16 == 0 && g.ldw % 16 == 0 && ((uintptr_t)g.A & 15) == 0 &&
+                ((uintptr_t)g.Wt & 15) == 0)
+                rc = kr_gemm_launch_wide(g, eps[j], s);
+            else if (g.M >= 4096 && (g.K >> 1) % 64 == 0) rc = launch_big<true>(g, eps[j], s);
             else if (g.M >= 4096) rc = launch_tile<128, 128, true>(g, eps[j], s);
             else rc = launch_tile<64, 64, true>(g, eps[j], s);
         } else if (g.K % 256 == 0 && (g.M >= 4096 || (g.M >= 128 && g.N >= KR_GEMM_SMALL_MAX_N))) {
@@ -1400,199 +1351,3 @@ int kr_det_matmul_packed(const uint16_t* xf, int M, int K, const uint16_t* Wf, i
 }
 
 }  // extern "C"
-
-// ---------------------------------------------------------------------------
-// Large-M head. A template instantiated by the last function of this file,
-// so the compiler emits it after every other kernel of the code object and
-// leaves their offsets as they were. Measured on MI355X (A B C on one box):
-// the same kernel emitted ahead of the panel kernels moved them by 13 KB and
-// the decode step's panel launches ran up to 6% slower (w8a8 decode -3%);
-// emitted last, decode is within 1% of the build without it.
-// ---------------------------------------------------------------------------
-namespace {
-
-// ---------------------------------------------------------------------------
-// Large-M head (compress: blocks of up to 8192 rows x V = 50277 columns,
-// K = C), under the head's one-chain contract. With no slice partials a
-// wave's 64 x 128 output block needs 128 accumulator registers, so a 512-thread
-// workgroup takes 256 x 256 tiles: (256 + 256) rows x 128 bytes per 64-wide
-// K step, two 64 KB stages. A workgroup's step costs about as many L2 line
-// requests as the 256 x 128 kernel's (512 against 384 lines) for twice the
-// MACs; the copies, not the MFMAs, set the time of both kernels (measured on
-// MI355X with timing copies: removing the copies -27%, the MFMAs, the
-// fragment reads or the per-step barrier within 3%). Measured at 8192 x 50277
-// x 768: 0.94-0.97 PF/s against 0.78-0.82 for the 256 x 128 slice-contract
-// kernel. Persistent like gemm_big_kernel (the same XCD-aware tile order);
-// one copy step in flight.
-// Copies: wave w < 4 copies A rows, w >= 4 W rows, 8 rows x 128 bytes per
-// instruction (the swizzled stage layout big_pos), from a wave-uniform base
-// plus a 32-bit byte offset (the host keeps every offset below 2^31).
-constexpr int kHeadBigStageUnits = 512 * 8;      // 16-byte units per 64 KB stage
-
-__device__ __forceinline__ void head_copy(const void* base, unsigned off, unsigned lds) {
-    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2"
-                 :: "s"(lds), "v"(off), "s"(base) : "memory", "m0");
-}
-
-__device__ __forceinline__ bool head_big_tile(int M, int N, int vb, int group_m, int& m_t, int& n_t) {
-    const int gy = (M + 255) / 256, gx = (N + 255) / 256;
-    const int T = gx * gy, per = (T + 7) / 8;
-    const int t = (vb & 7) * per + (vb >> 3);
-    if (t >= T || (vb >> 3) >= per) return false;
-    const int in_group = group_m * gx;
-    const int first_m = (t / in_group) * group_m;
-    const int gm = min(gy - first_m, group_m);
-    const int r = t % in_group;
-    m_t = first_m + r % gm;
-    n_t = r / gm;
-    return true;
-}
-
-template <int KSTEP>   // 64: the K step of the copy ring
-__global__ void __launch_bounds__(512, 1) gemm_head_big_kernel(
-        const kr_half* __restrict__ A, long long lda, const kr_half* __restrict__ Wt, long long ldw,
-        kr_half* __restrict__ out, long long ldo, int M, int N, int K, int n_virtual, int group_m) {
-    __shared__ __attribute__((aligned(1024))) kr_half8 ring[2 * kHeadBigStageUnits];
-    const int tid = threadIdx.x, lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wm = wave >> 1, wn = wave & 1;        // 4 x 2 waves of 64 x 128
-    const int G = gridDim.x;
-    static_assert(KSTEP == 64, "one 128-byte row segment per copy");
-    const int KS = K / KSTEP;
-    const unsigned ring_base = (unsigned)(uintptr_t)(__attribute__((address_space(3))) char*)ring;
-    const bool a_wave = wave < 4;
-    const kr_half* base = a_wave ? A : Wt;
-    const long long ld = a_wave ? lda : ldw;
-    const int lim = a_wave ? M : N;
-    // copy i of this wave, tile rows from r0 of its operand: stage rows
-    // 8 (8 w + i) .. + 7 (W rows after the 256 A rows), lane l moving chunk
-    // (l % 8) ^ ((row / 2) % 8) of row 8 (8 w + i) % 256 + l / 8
-    auto issue = [&](int r0, int ks, int q) {
-        const unsigned so = ring_base + (unsigned)((q & 1) * kHeadBigStageUnits * 16);
-        #pragma unroll
-        for (int i = 0; i < 8; i++) {
-            const int crow = 8 * ((wave * 8 + i) & 31) + (lane >> 3);
-            const int ckc = (lane & 7) ^ ((crow >> 1) & 7);
-            const unsigned off = (unsigned)((long long)min(r0 + crow, lim - 1) * ld * 2) +
-                                 (unsigned)(ckc * 16 + ks * 128);
-            head_copy(base, off, so + (unsigned)((wave * 8 + i) * 1024));
-        }
-    };
-    int vb = blockIdx.x, m_t, n_t;
-    if (!head_big_tile(M, N, vb, group_m, m_t, n_t)) return;
-    int r0 = a_wave ? m_t * 256 : n_t * 256, nr0 = 0;
-    int q = 0;
-    issue(r0, 0, 0);
-    int stores_behind = 0;   // vector stores of the previous tile, behind this tile's first copies
-    const bool vec_ok = (ldo & 3) == 0 && ((uintptr_t)out & 7) == 0;
-    const int lr = lane & 15, lq = lane >> 4;
-    while (true) {
-        const int m0 = m_t * 256, n0 = n_t * 256;
-        int nm_t = 0, nn_t = 0;
-        const bool has_next = vb + G < n_virtual && head_big_tile(M, N, vb + G, group_m, nm_t, nn_t);
-        if (has_next) nr0 = a_wave ? nm_t * 256 : nn_t * 256;
-        kr_float4 acc[4][8];
-        #pragma unroll
-        for (int i = 0; i < 4; i++)
-            #pragma unroll
-            for (int t = 0; t < 8; t++) acc[i][t] = kr_float4{0, 0, 0, 0};
-        #pragma unroll 1
-        for (int ks = 0; ks < KS; ks++, q++) {
-            // step q's copies are in once at most the previous tile's stores
-            // (issued after them, counted in a tile's first step) remain
-            if (ks == 0 && stores_behind == 32) asm volatile("s_waitcnt vmcnt(32)" ::: "memory");
-            else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-            __syncthreads();   // every wave's copies of step q are in; step q-1's stage is free
-            if (ks + 1 < KS) issue(r0, ks + 1, q + 1);
-            else if (has_next) issue(nr0, 0, q + 1);
-            const kr_half8* As = ring + (q & 1) * kHeadBigStageUnits;
-            const kr_half8* Ws = As + 256 * 8;
-            #pragma unroll
-            for (int kb = 0; kb < 2; kb++) {
-                kr_half8 a[4];
-                #pragma unroll
-                for (int i = 0; i < 4; i++) a[i] = As[big_pos(64 * wm + 16 * i + lr, 4 * kb + lq)];
-                #pragma unroll
-                for (int th = 0; th < 2; th++) {
-                    // four weight fragments at a time (register budget)
-                    __builtin_amdgcn_sched_barrier(0);
-                    kr_half8 w[4];
-                    #pragma unroll
-                    for (int t = 0; t < 4; t++)
-                        w[t] = Ws[big_pos(128 * wn + 16 * (4 * th + t) + lr, 4 * kb + lq)];
-                    __builtin_amdgcn_sched_barrier(0);
-                    #pragma unroll
-                    for (int i = 0; i < 4; i++)
-                        #pragma unroll
-                        for (int t = 0; t < 4; t++)
-                            acc[i][4 * th + t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-                                w[t], a[i], acc[i][4 * th + t], 0, 0, 0);
-                }
-            }
-        }
-        // lane: row 64 wm + 16 i + lane % 16, columns 128 wn + 16 t + 4 (lane / 16) .. + 3
-        const bool full = m0 + 256 <= M && n0 + 256 <= N;
-        #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int m = m0 + 64 * wm + 16 * i + lr;
-            if (!full && m >= M) continue;
-            #pragma unroll
-            for (int t = 0; t < 8; t++) {
-                const int n = n0 + 128 * wn + 16 * t + 4 * lq;
-                kr_half* dst = out + (size_t)m * (size_t)ldo + n;
-                if (vec_ok && n + 3 < N) {
-                    kr_half4 h;
-                    #pragma unroll
-                    for (int r = 0; r < 4; r++) h[r] = kr_f16(acc[i][t][r]);
-                    *reinterpret_cast<kr_half4*>(dst) = h;
-                } else {
-                    #pragma unroll
-                    for (int r = 0; r < 4; r++)
-                        if (n + r < N) dst[r] = kr_f16(acc[i][t][r]);
-                }
-            }
-        }
-        if (!has_next) break;
-        // a whole tile with vector access ends in exactly 32 stores per wave
-        stores_behind = full && vec_ok ? 32 : 0;
-        vb += G;
-        m_t = nm_t;
-        n_t = nn_t;
-        r0 = nr0;
-    }
-}
-
-}  // namespace
-
-// Row tiles per group of the large-M head's tile order: 3 measured fastest
-// on MI355X at 8192 x 50277 x 768 (652-668 us per launch; 1: 687-709, 5:
-// 669-673, 8: 703-707).
-constexpr int kHeadBigGroupM = 3;
-
-int kr_gemm_head_big(const kr_half* A, long long lda, const kr_half* Wt, long long ldw, int M,
-                     int N, int K, kr_half* out, long long ldo, hipStream_t s) {
-    KR_REQUIRE(A && Wt && out, "head: null pointer");
-    KR_REQUIRE(M >= 0 && N >= 1 && K >= 64 && K % 64 == 0,
-               "head: unsupported M=%d N=%d K=%d (K must be a multiple of 64)", M, N, K);
-    KR_REQUIRE(lda >= K && ldw >= K && lda % 8 == 0 && ldw % 8 == 0,
-               "head: lda %lld / ldw %lld must be >= K and multiples of 8", lda, ldw);
-    KR_REQUIRE(ldo >= N, "head: ldo %lld < N %d", ldo, N);
-    KR_REQUIRE(((uintptr_t)A & 15) == 0 && ((uintptr_t)Wt & 15) == 0,
-               "head: operands must be 16-byte aligned");
-    KR_REQUIRE((long long)N * ldw * 2 < (1ll << 31), "head: weights of 2 GB or more");
-    // the kernel addresses its operands by 32-bit byte offsets: rows of A in
-    // blocks that keep them below 2^31 (a row's bits do not depend on M)
-    const long long rows_max = ((1ll << 31) / (lda * 2)) / 256 * 256;
-    KR_REQUIRE(rows_max >= 256, "head: lda %lld too large", lda);
-    for (long long r0 = 0; r0 < M; r0 += rows_max) {
-        const int m = (int)std::min<long long>(rows_max, M - r0);
-        const long long T = (long long)((N + 255) / 256) * ((m + 255) / 256);
-        const int n_virtual = (int)((T + 7) / 8 * 8);
-        const int grid = n_virtual < 256 ? n_virtual : 256;   // one workgroup per CU
-        gemm_head_big_kernel<64><<<grid, 512, 0, s>>>(A + r0 * lda, lda, Wt, ldw, out + r0 * ldo, ldo, m,
-                                                  N, K, n_virtual, kHeadBigGroupM);
-        KR_LAUNCHED();
-    }
-    return KR_OK;
-}
-

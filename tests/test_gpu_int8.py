@@ -113,6 +113,36 @@ def test_int8_epilogues(ep, packed):
         assert np.array_equal(got, want)
 
 
+@pytest.mark.parametrize("ep", [0, 1, 2, 3, 4, 5])
+def test_int8_large_m_epilogues(ep):
+    """The large-M int8 path for wide products (256 x 256 tiles, exact int32
+    sums) with every epilogue, on ragged row and column tiles (M = 4200,
+    N = 2100): the exact integer product, dequantised and passed through the
+    epilogue, bit for bit (sigmoid within an fp16 ulp)."""
+    M, K, N = 4200, 768, 2100
+    g = torch.Generator().manual_seed(100 + ep)
+    qa = torch.randint(-127, 128, (M, K), generator=g, dtype=torch.int8)
+    qw = torch.randint(-127, 128, (N, K), generator=g, dtype=torch.int8)
+    sa = torch.rand(M, generator=g) * 1e-3
+    sw = torch.rand(N, generator=g) * 1e-3
+    res = torch.randn(M, N, generator=g).half()
+    gate = torch.rand(M, N, generator=g).half()
+    y = quant.matmul_i8(qa.numpy(), sa.numpy(), qw.numpy(), sw.numpy())
+    want = y if ep == 0 else _ref_epilogue(ep, y, res.numpy(), gate.numpy())
+    xa, wb = qa.to(DEV), qw.to(DEV)
+    out = torch.empty(M, N, dtype=torch.float32, device=DEV) if ep == 0 else res.clone().to(DEV)
+    sa_d, sw_d, gate_d = sa.to(DEV), sw.to(DEV), gate.to(DEV)   # kept alive across the launch
+    res_ptr = out.data_ptr() if ep in (4, 5) else None
+    _lib.call("kr_det_matmul_i8", xa.data_ptr(), sa_d.data_ptr(), M, K, wb.data_ptr(),
+              sw_d.data_ptr(), N, out.data_ptr(), N, ep, res_ptr, gate_d.data_ptr(), 0,
+              _lib.stream_ptr())
+    got = out.cpu().numpy()
+    if ep == 2:
+        np.testing.assert_allclose(got.astype(np.float32), want.astype(np.float32), rtol=1e-3, atol=1e-3)
+    else:
+        assert np.array_equal(got, want)
+
+
 def _pack_f16(x16: torch.Tensor):
     """fp16 [M, K] -> fragment-packed (kr_pack_fragments), rows padded to 16."""
     M, K = x16.shape
