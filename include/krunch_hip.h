@@ -339,7 +339,10 @@ int kr_forward_layers(const kr_model_weights* m, void* x, int B, int T, void* st
 /* x[row] = emb[ids[row]] (cpp_path.py:154,450). */
 int kr_embed(const kr_model_weights* m, const int32_t* ids, int M, void* x, void* stream);
 
-/* logits [M, ld] fp16 = LN_out(x) @ head (cpp_path.py:161-163); xn: [M, C] scratch. */
+/* logits [M, ld] fp16 = LN_out(x) @ head (cpp_path.py:161-163); xn: [M, C] scratch.
+ * The head has a reduction of its own: for every logit one chain of
+ * v_mfma_f32_16x16x32_f16 over the whole K = C from zero, then fp16; the
+ * same bits for any M, with or without headF (decode and compress agree). */
 int kr_head_logits(const kr_model_weights* m, const void* x, int M, void* xn, void* logits,
                    long long ld, void* stream);
 
