@@ -980,27 +980,38 @@ int launch_small(const kr_gemm_multi& mj, hipStream_t s) {
 //
 // The persistent 256x128 kernel re-reads all M rows of A for every
 // 128-column tile: 393 tiles at V = 50277 over 256 CUs, 9,216 L2 lines on the
-// busiest CU. Here wave w holds row blocks 2w, 2w + 1 of the fragment-packed
-// A (2 x K/32 fragments, 8 K/32 VGPRs), so a CU reads A once plus its share
-// of the weights (~5,400 lines). A weight block (16 columns x K, contiguous
-// in the fragment layout) goes into an LDS ring of kHeadStages stages by
-// asynchronous copies issued kHeadStages - 1 blocks ahead; all eight waves
-// multiply each block with their rows.
+// busiest CU. Here a workgroup of four waves takes one group of 64 RBW rows
+// (wave w: row blocks RBW w .. RBW w + RBW - 1 of the group, RBW x K/32
+// fragments of the fragment-packed A held in registers) and one contiguous
+// run of 16-column weight blocks, which it streams once: a weight block (16
+// columns x K, contiguous in the fragment layout) goes into an LDS ring of
+// kHeadStages stages by asynchronous copies issued kHeadStages - 1 blocks
+// ahead, and all four waves multiply each block with their rows. The mh row
+// groups of one column run are workgroups b, b + 8, ..., which the dispatcher
+// places on one XCD, so its L2 fetches each weight block once for all of them.
 // The head's reduction contract (kr_gemm.h, the head): one
 // v_mfma_f32_16x16x32_f16 chain over the whole K from zero, MFMA issued as
-// W^T x A^T, then out = fp16(acc); gemm_head_big_kernel gives the same bits.
+// W^T x A^T, then out = fp16(acc); gemm_wide_kernel gives the same bits.
 constexpr int kHeadStages = 4;
-// Row blocks per wave: 4 (four waves, A in VGPRs + AGPRs, each weight
-// fragment read from LDS feeds 4 MFMAs) measured 1.3% faster per decode step
-// on MI355X than 2 (eight waves, 2 MFMAs per fragment read).
-constexpr int kHeadRBW = 4;
+// Row blocks per wave. Every weight block needs all of a workgroup's A in
+// registers, so the A load (all rows of the group) is not overlapped by any
+// MFMA; two row groups of 128 rows halve it and double each CU's weight
+// stream. Measured on MI355X at M = 256 (A B on three boxes, decode KB/s):
+// 2 row blocks per wave with two row groups 2,015 / 2,025 / 2,030 against
+// 1,972 / 1,989 / 2,017 for 4 (one group of 256 rows); the isolated launch
+// 28.0-28.4 us against 28.7-29.9 with the weights in the memory-side cache
+// and 33.4 against 37.9-38.4 without. The two row groups on different XCDs
+// (weights fetched into two L2s): 1,915. A 6-stage ring or two workgroups
+// per CU (3 stages each): 2,008 / 2,012 against 2,025.
+constexpr int kHeadRBW = 2;
 
-// RBW row blocks (16 rows) per wave, 16 / RBW waves: 256 rows per workgroup.
+// RBW row blocks (16 rows) per wave, four waves: 64 RBW rows per workgroup;
+// mh row groups share each column run (gridDim.x = mh x the runs).
 template <int KB, int RBW>   // KB = K / 32 fragments per row: K = 256, 512 or 768
-__global__ void __launch_bounds__(1024 / RBW, 1) gemm_head_small_kernel(
+__global__ void __launch_bounds__(256, 1) gemm_head_small_kernel(
         const kr_half* __restrict__ Af, const kr_half* __restrict__ Wf, kr_half* __restrict__ out,
-        long long ldo, int M, int N, int vec) {
-    constexpr int NW = 16 / RBW;     // waves
+        long long ldo, int M, int N, int vec, int mh) {
+    constexpr int NW = 4;            // waves
     constexpr int CPW = KB / NW;     // 1 KB copies per wave per block
     constexpr int S = KB / 8;        // groups of 8 fragments (256 k) per LDS wait
     constexpr int AHEAD = (kHeadStages - 2) * CPW;
@@ -1009,12 +1020,23 @@ __global__ void __launch_bounds__(1024 / RBW, 1) gemm_head_small_kernel(
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
     const int nb_total = (N + 15) >> 4;
-    const int b0 = (int)(((long long)blockIdx.x * nb_total) / gridDim.x);
-    const int b1 = (int)(((long long)(blockIdx.x + 1) * nb_total) / gridDim.x);
+    // row group h and column run cr of this workgroup: with a multiple of 8
+    // runs, the groups of run cr are workgroups 8 mh (cr / 8) + cr % 8 + 8 h
+    const int bx = blockIdx.x, ncr = (int)gridDim.x / mh;
+    int h, cr;
+    if ((ncr & 7) == 0) {
+        h = (bx >> 3) % mh;
+        cr = (bx / (8 * mh)) * 8 + (bx & 7);
+    } else {
+        h = bx % mh;
+        cr = bx / mh;
+    }
+    const int b0 = (int)(((long long)cr * nb_total) / ncr);
+    const int b1 = (int)(((long long)(cr + 1) * nb_total) / ncr);
     const int nblk = b1 - b0;
     // this wave's rows (row blocks past the last one re-read it; never stored)
     const int last_mb = (M - 1) >> 4;
-    const int mb0 = RBW * wave;
+    const int mb0 = h * (RBW * NW) + RBW * wave;
     const bool active = mb0 <= last_mb;
     kr_half8 a[RBW][KB];
     if (active) {
@@ -1142,12 +1164,15 @@ int kr_gemm_head_small(const kr_half* Af, const kr_half* Wf, int M, int N, int K
                "head: operands must be 16-byte aligned");
     const int vec = (ldo & 3) == 0 && ((uintptr_t)out & 7) == 0;
     const int nb = (N + 15) / 16;
-    const int grid = nb < 256 ? nb : 256;
     constexpr int R = kHeadRBW;
+    // row groups of 64 R rows, and column runs: one workgroup per CU
+    const int mh = (M + 64 * R - 1) / (64 * R);
+    const int ncr = nb < 256 / mh ? nb : 256 / mh;
+    const int grid = ncr * mh;
     switch (K) {
-        case 256: gemm_head_small_kernel<8, R><<<grid, 1024 / R, 0, s>>>(Af, Wf, out, ldo, M, N, vec); break;
-        case 512: gemm_head_small_kernel<16, R><<<grid, 1024 / R, 0, s>>>(Af, Wf, out, ldo, M, N, vec); break;
-        default: gemm_head_small_kernel<24, R><<<grid, 1024 / R, 0, s>>>(Af, Wf, out, ldo, M, N, vec); break;
+        case 256: gemm_head_small_kernel<8, R><<<grid, 256, 0, s>>>(Af, Wf, out, ldo, M, N, vec, mh); break;
+        case 512: gemm_head_small_kernel<16, R><<<grid, 256, 0, s>>>(Af, Wf, out, ldo, M, N, vec, mh); break;
+        default: gemm_head_small_kernel<24, R><<<grid, 256, 0, s>>>(Af, Wf, out, ldo, M, N, vec, mh); break;
     }
     KR_LAUNCHED();
     return KR_OK;

@@ -1261,9 +1261,10 @@ int kr_impl_embed(const kr_model_weights* m, const int32_t* ids, int M, void* x,
 int kr_impl_head(const kr_model_weights* m, const void* x, int M, void* xn, void* logits,
                  long long ld, hipStream_t s, bool xn_rows16) {
     if (M == 0) return KR_OK;
-    // up to 512 rows as launches of <= 256 rows (A of 256 rows is what one
-    // workgroup holds in registers); measured at 512 rows on MI355X, two
-    // small-M launches beat one 256x128 launch (2 x ~30 us against 66.8 us)
+    // up to 512 rows as launches of <= 256 rows (the small-M kernel takes two
+    // groups of 128 rows, each held in registers by its workgroups); measured
+    // at 512 rows on MI355X, two small-M launches beat one 256x128 launch
+    // (2 x ~30 us against 66.8 us)
     constexpr int kHeadChunk = 256;
     const bool small = xn_rows16 && m->headF && M <= 2 * kHeadChunk &&
                        kr_gemm_head_small_ok(std::min(M, kHeadChunk), m->V, m->C);
