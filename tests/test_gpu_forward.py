@@ -183,6 +183,40 @@ def test_small_head_equals_tiled_head(model, M):
     assert (outs[0][:, :P.V].float() - ref).abs().max() < 2e-2
 
 
+@pytest.mark.parametrize("C,V,M,pad", [(256, 1000, 144, 8), (512, 1000, 256, 3),
+                                       (768, 2051, 144, 8), (768, 1000, 48, 3)])
+def test_small_head_small_vocab(C, V, M, pad):
+    """The decode head where the vocabulary has fewer 16-column blocks than
+    the launch has column runs for (63 runs: row groups and runs dealt in
+    workgroup order; 129 blocks: 128 runs of one or two blocks), with a
+    second row group of 16 rows (M = 144), one group (M = 48), K = 256, 512
+    and 768, vector and scalar stores: the large-M head's bits."""
+    from krunch_amd import _lib
+    import ctypes
+    w16 = synthetic.make_weights(n_layer=1, C=C, F=2 * C, V=V, seed=C + V)
+    W = cpp_path.init_weights(w16, "cuda")
+    try:
+        P = W["prepared"]
+        m_row, _keep = _row_major_only(P)
+        g = torch.Generator(device="cpu").manual_seed(M)
+        x = torch.randn((M, C), generator=g).half().cuda()
+        ld = V + pad
+        outs = []
+        for mdesc in (P.model_c, m_row):
+            xn = torch.empty((M, C), dtype=torch.float16, device="cuda")
+            logits = torch.full((M, ld), float("nan"), dtype=torch.float16, device="cuda")
+            _lib.call("kr_head_logits", ctypes.byref(mdesc), x.data_ptr(), M, xn.data_ptr(),
+                      logits.data_ptr(), ld, _lib.stream_ptr())
+            outs.append(logits)
+        assert torch.equal(outs[0][:, :V], outs[1][:, :V])
+        assert torch.isnan(outs[0][:, V:]).all()
+        ref = torch.nn.functional.layer_norm(x.float(), (C,), eps=1e-5) @ \
+            P.tensors["headT"].float().t()
+        assert (outs[0][:, :V].float() - ref).abs().max() < 2e-2
+    finally:
+        cpp_path.release_weights(w16)
+
+
 @pytest.mark.parametrize("M", [1000, 4096 + 37])
 def test_large_m_head_rows_equal_decode_head_rows(model, M):
     """A row's logits are the same bits whichever head kernel computes it and
