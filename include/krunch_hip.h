@@ -253,7 +253,7 @@ typedef struct kr_model_weights {
     const void* headT;                    /* fp16 [V, C] */
     const kr_layer_weights* layers;       /* host array, n_layer entries */
     /* Fragment-packed copy of headT (kr_pack_fragments), read by the decode
-     * head (M <= 256 rows, C <= 768); NULL = the row-major head. */
+     * head (M <= 512 rows, C <= 768); NULL = the row-major head. */
     const void* headF;
 } kr_model_weights;
 

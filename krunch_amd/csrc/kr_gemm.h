@@ -142,7 +142,7 @@ int kr_gemm_launch_multi(const kr_gemm_args* jobs, const int* epilogues, int njo
 // costs it nothing; the large-M head gains a 256 x 256 tile from the
 // registers the slice partials would take.
 
-// out[M, N] (row stride ldo) = fp16(A @ W) for the small-M head (M <= 256,
+// out[M, N] (row stride ldo) = fp16(A @ W) for the small-M head (M <= 512,
 // K in {256, 512, 768}): A fragment-packed [M rows padded to 16, K], W^T
 // fragment-packed [N padded to 16, K].
 bool kr_gemm_head_small_ok(int M, int N, int K);

@@ -974,7 +974,7 @@ int launch_small(const kr_gemm_multi& mj, hipStream_t s) {
 }
 
 // ---------------------------------------------------------------------------
-// Small-M head (the decode step: M <= 256 rows x V = 50277 columns, K = C):
+// Small-M head (the decode step: M <= 512 rows x V = 50277 columns, K = C):
 // the A operand stays in registers for the whole launch and each workgroup
 // streams its own contiguous run of 16-column weight blocks exactly once.
 //
@@ -1152,7 +1152,7 @@ __global__ void transpose_kernel(const kr_half* __restrict__ W, long long ldw_in
 }  // namespace
 
 bool kr_gemm_head_small_ok(int M, int N, int K) {
-    return M >= 1 && M <= 256 && N >= 1 && (K == 256 || K == 512 || K == 768);
+    return M >= 1 && M <= 512 && N >= 1 && (K == 256 || K == 512 || K == 768);
 }
 
 int kr_gemm_head_small(const kr_half* Af, const kr_half* Wf, int M, int N, int K, kr_half* out,

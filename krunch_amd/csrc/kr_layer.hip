@@ -1261,13 +1261,12 @@ int kr_impl_embed(const kr_model_weights* m, const int32_t* ids, int M, void* x,
 int kr_impl_head(const kr_model_weights* m, const void* x, int M, void* xn, void* logits,
                  long long ld, hipStream_t s, bool xn_rows16) {
     if (M == 0) return KR_OK;
-    // up to 512 rows as launches of <= 256 rows (the small-M kernel takes two
-    // groups of 128 rows, each held in registers by its workgroups); measured
-    // at 512 rows on MI355X, two small-M launches beat one 256x128 launch
-    // (2 x ~30 us against 66.8 us)
-    constexpr int kHeadChunk = 256;
-    const bool small = xn_rows16 && m->headF && M <= 2 * kHeadChunk &&
-                       kr_gemm_head_small_ok(std::min(M, kHeadChunk), m->V, m->C);
+    // up to 512 rows in one small-M launch (groups of 128 rows, each held in
+    // registers by its workgroups). Measured at 512 rows on MI355X: two
+    // 256-row small-M launches took 2 x ~30 us against 66.8 us for one
+    // 256x128 launch, and one 512-row launch decodes 0.7% faster than the two
+    // (B = 512, A B twice on one box).
+    const bool small = xn_rows16 && m->headF && kr_gemm_head_small_ok(M, m->V, m->C);
     LnMixArgs a{};
     a.x = H(x);
     a.ln_w = H(m->ln_out_w);
@@ -1278,14 +1277,7 @@ int kr_impl_head(const kr_model_weights* m, const void* x, int M, void* xn, void
     a.run = 1;
     a.frag = small ? 1 : 0;
     KR_TRY(launch_ln_mix<0>(m->C / 256, a, s));
-    if (small) {
-        // fragment-packed rows r0.. start at element r0 * C (r0 a multiple of 16)
-        for (int r0 = 0; r0 < M; r0 += kHeadChunk)
-            KR_TRY(kr_gemm_head_small(H(xn) + (size_t)r0 * m->C, H(m->headF),
-                                      std::min(kHeadChunk, M - r0), m->V, m->C,
-                                      Hm(logits) + (size_t)r0 * (size_t)ld, ld, s));
-        return KR_OK;
-    }
+    if (small) return kr_gemm_head_small(H(xn), H(m->headF), M, m->V, m->C, Hm(logits), ld, s);
     return kr_gemm_head_big(H(xn), m->C, H(m->headT), m->C, M, m->V, m->C, Hm(logits), ld, s);
 }
 

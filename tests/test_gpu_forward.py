@@ -157,7 +157,7 @@ def test_pack_fragments_layout():
 @pytest.mark.parametrize("M", [16, 48, 256, 400, 512])
 def test_small_head_equals_tiled_head(model, M):
     """The decode head (A held in registers, fragment-packed weights streamed
-    once; 256-row launches up to 512 rows) gives the large-M head kernel's
+    once; one launch up to 512 rows) gives the large-M head kernel's
     logits (256 x 256 tiles, row-major operands) bit for bit: the head's
     one-chain contract. Includes the 5-column tail block of V = 50277 and a
     padded row stride."""
