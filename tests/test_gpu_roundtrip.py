@@ -41,8 +41,8 @@ def test_roundtrip_ragged_streams(eng):
 @pytest.mark.parametrize("B", [37, 200, 300])
 def test_roundtrip_many_streams(eng, B):
     """Decode steps of 37, 200 and 300 streams: the decode head's last row
-    block is partial; at 200 several of its waves hold rows and one holds
-    part; at 300 the head runs as a 256-row and a 44-row launch."""
+    block is partial; at 200 its second row group holds 72 rows; at 300 it
+    runs three row groups of 128 rows per column run, the last holding 44."""
     toks = [synthetic.zipf_tokens(1, 12 + (i % 5), seed_base=1300 + i)[0] for i in range(B)]
     enc = eng.compress_tokens_batched(toks)
     dec = eng.decompress_tokens_batched(enc)
