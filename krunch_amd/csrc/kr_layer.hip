@@ -494,7 +494,9 @@ int launch_ln_mix(int G, const LnMixArgs& a_in, hipStream_t s) {
 
 // Tile shape of the fused K, V, R + WKV launch: the fewest operand lines on
 // the busiest CU (workgroups spread over 256 CUs, each reading 3 x (16*TM +
-// 16*NS) rows of C), ties to more workgroups.
+// 16*NS) rows of C), ties to more workgroups. 3 x 2 serves 342..384 rows in
+// one round of workgroups where 2 x 2 needs two (measured on MI355X at
+// B = 384: decode +4.5%, A B twice on one box).
 template <int S, int TM, int NS, bool I8>
 int launch_kvr_wkv_shape(const KvrWkvArgs& a, hipStream_t s) {
     const int mt = (a.M + 16 * TM - 1) / (16 * TM);
@@ -504,14 +506,14 @@ int launch_kvr_wkv_shape(const KvrWkvArgs& a, hipStream_t s) {
     return KR_OK;
 }
 
-constexpr int kKvrShapes[4][2] = {{2, 2}, {2, 1}, {1, 2}, {1, 1}};   // (TM, NS)
+constexpr int kKvrShapes[5][2] = {{2, 2}, {2, 1}, {1, 2}, {1, 1}, {3, 2}};   // (TM, NS)
 
 // Shape of the K/V/R + WKV launch for M rows and C = 256 S channels (index
 // into kKvrShapes): busiest-CU line model, ties to more workgroups.
 int kvr_wkv_shape(int S, int M) {
     long long best = -1;
     int bi = 0;
-    for (int i = 0; i < 4; i++) {
+    for (int i = 0; i < 5; i++) {
         const int TM = kKvrShapes[i][0], NS = kKvrShapes[i][1];
         const long long wgs = (long long)((M + 16 * TM - 1) / (16 * TM)) * (256 * S / (16 * NS));
         const long long cost = ((wgs + 255) / 256) * (TM + NS) * 4096 - std::min(wgs, 256ll);
@@ -526,6 +528,7 @@ int launch_kvr_wkv_s(const KvrWkvArgs& a, hipStream_t s) {
         case 0: return launch_kvr_wkv_shape<S, 2, 2, I8>(a, s);
         case 1: return launch_kvr_wkv_shape<S, 2, 1, I8>(a, s);
         case 2: return launch_kvr_wkv_shape<S, 1, 2, I8>(a, s);
+        case 4: return launch_kvr_wkv_shape<S, 3, 2, I8>(a, s);
         default: return launch_kvr_wkv_shape<S, 1, 1, I8>(a, s);
     }
 }

@@ -111,10 +111,11 @@ def _row_major_only(P):
     return m, layers
 
 
-@pytest.mark.parametrize("B", [1, 37, 256])
+@pytest.mark.parametrize("B", [1, 37, 256, 360])
 def test_fragment_path_equals_row_major_path(model, B):
     """Small-M layers with fragment-packed operands give the row-major
-    path's bits (outputs and carried state), over two steps."""
+    path's bits (outputs and carried state), over two steps. At 360 rows the
+    fused K/V/R + WKV launch takes 3 x 2 tiles."""
     from krunch_amd import _lib
     import ctypes
     _, W = model

@@ -47,13 +47,14 @@ def _gpu_and_oracles(model, B=2, T=24):
     return got, q16, f32
 
 
-@pytest.mark.parametrize("B,T", [(2, 24), (3, 64), (4, 1), (256, 1), (1, 600), (2, 2100)])
+@pytest.mark.parametrize("B,T", [(2, 24), (3, 64), (4, 1), (256, 1), (360, 1), (1, 600), (2, 2100)])
 def test_w8a8_layers_bit_exact_vs_int8_oracle(model, B, T):
     """Teacher forcing: every layer of the GPU's int8 codec (kr_layer_step:
     LN-mix with int8 outputs, int8 K/V/R + WKV, the output and value products
     quantising their fp16 operands on load) fed the GPU's own input rows and a
-    fresh state gives exactly the oracle layer's output and state. B = 256,
-    T = 1 runs the decode step's fused kernels; T > 1 the packed ones (M =
+    fresh state gives exactly the oracle layer's output and state. B = 256
+    and 360, T = 1 run the decode step's fused kernels (at 360 rows the fused
+    K/V/R + WKV launch takes 3 x 2 tiles); T > 1 the packed ones (M =
     600: the row quantiser and the tiled int8 GEMM; M = 4200: the persistent
     256 x 128 int8 GEMM)."""
     w16, W = model
