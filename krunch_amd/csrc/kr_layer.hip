@@ -494,7 +494,7 @@ int launch_ln_mix(int G, const LnMixArgs& a_in, hipStream_t s) {
 
 // Tile shape of the fused K, V, R + WKV launch: the fewest operand lines on
 // the busiest CU (workgroups spread over 256 CUs, each reading 3 x (16*TM +
-// 16*NS) rows of C), ties to more workgroups. 3 x 2 serves 342..384 rows in
+// 16*NS) rows of C), ties to more workgroups. 3 x 2 serves 342..480 rows in
 // one round of workgroups where 2 x 2 needs two (measured on MI355X at
 // B = 384: decode +4.5%, A B twice on one box).
 template <int S, int TM, int NS, bool I8>
