@@ -404,13 +404,16 @@ ROOFLINE_TRACE = os.path.join(ROOT, "profiles", "decode_step_B256_roofline.json"
 
 
 def _roofline_entry(kernel, alg_bytes, us_isolated, step, phase_key, traffic_file, B):
-    """`frac` from the launch's average duration inside the decode step as a
-    kernel trace of this bench measures it (dispatch to completion; recorded
-    by `bench.py --hbm-table ... --roofline-json` in ROOFLINE_TRACE, at B =
-    256). Beside it, measured live in this run: the launch's in-step wave span
-    (step_timed_launches; the trace file records the span of the profiled
-    run, so `trace_matches_build` says whether this build runs the launch as
-    the traced one did, within 5%) and the isolated HIP-event figure."""
+    """`frac` from the launch's average duration inside the decode step of
+    this run: its in-step wave span measured live (step_timed_launches: first
+    wave start to last wave end on the steady counter, graph launches) plus
+    the dispatch and teardown time a rocprofv3 kernel trace of this bench
+    adds to the span (the trace's mean launch duration minus the profiled
+    run's span, both recorded by `bench.py --hbm-table ... --roofline-json`
+    in ROOFLINE_TRACE, at B = 256). `trace_matches_build` says whether this
+    run's span is within 5% of the profiled run's. Without a live span the
+    trace's mean duration is used; without the trace file, the isolated
+    HIP-event figure, which is also reported beside it."""
     traffic = None
     tfile = os.path.join(ROOT, "profiles", traffic_file)
     if os.path.exists(tfile) and B == 256:
@@ -424,11 +427,21 @@ def _roofline_entry(kernel, alg_bytes, us_isolated, step, phase_key, traffic_fil
         with open(ROOFLINE_TRACE) as f:
             trace = json.load(f)["phases"].get(phase_key)
     span = mean(step["span"]) if step and step.get("span") else None
-    if trace:
+    rel = os.path.relpath(ROOFLINE_TRACE, ROOT)
+    if trace and span and trace.get("wave_span_us_same_run"):
+        over = trace["in_step_mean_us"] - trace["wave_span_us_same_run"]
+        us = span + over
+        timing = ("in the decode step of this run: the launch's mean in-step wave span %.3f us "
+                  "(graph launches, kr_step_timing) plus %.3f us of dispatch and teardown, the "
+                  "mean launch duration %.3f us of a rocprofv3 kernel trace of this bench "
+                  "minus that run's span %.3f us over its %d launches (%s)"
+                  % (span, over, trace["in_step_mean_us"], trace["wave_span_us_same_run"],
+                     trace["launches"], rel))
+    elif trace:
         us = trace["in_step_mean_us"]
         timing = ("in the decode step: mean duration of the %d launches of this kernel inside "
                   "the decode steps of a rocprofv3 kernel trace of this bench (%s)"
-                  % (trace["launches"], os.path.relpath(ROOFLINE_TRACE, ROOT)))
+                  % (trace["launches"], rel))
     else:
         us = us_isolated
         timing = "isolated: graph of 64 launches over 64 weight copies"
@@ -442,6 +455,8 @@ def _roofline_entry(kernel, alg_bytes, us_isolated, step, phase_key, traffic_fil
         out["in_step_wave_span_us"] = {"graph": round(span, 3),
                                        "eager": round(mean(step["span_eager"]), 3),
                                        "eager_dispatch_events": round(mean(step["events"]), 3)}
+    if trace:
+        out["trace_in_step_mean_us"] = trace["in_step_mean_us"]
     if trace and span and trace.get("wave_span_us_same_run"):
         ref = trace["wave_span_us_same_run"]
         out["trace_matches_build"] = bool(abs(span / ref - 1) <= 0.05)
@@ -459,9 +474,10 @@ def dominant_kernel_roofline(weights16, B, in_step=None):
       * the channel-mix value product (M = B, K = 3072, N = 768, gated
         residual), W 3072 * 768 * 2 + A B * 3072 * 2 + residual, gate and
         output 3 * B * 768 * 2.
-    `frac` comes from each launch's average duration inside the decode step
-    in a kernel trace of this bench (ROOFLINE_TRACE), with the live in-step
-    wave span and the isolated figure beside it (_roofline_entry). The
+    `frac` comes from each launch's average duration inside this run's
+    decode step: the live in-step wave span plus the dispatch and teardown a
+    kernel trace of this bench adds to it (ROOFLINE_TRACE), with the isolated
+    figure beside it (_roofline_entry). The
     isolated figure: the launch as the decode step launches it
     (fragment-packed operands), in a captured
     graph of 64 launches over 64 distinct weight copies (> the 256 MB
@@ -534,7 +550,8 @@ def dominant_kernel_roofline(weights16, B, in_step=None):
 
 # Algorithmic bytes of each phase of one stepped decode step (B streams,
 # C = 768, F = 3072, V = 50277, fp16 activations and weights, fp32 WKV
-# state); see DESIGN.md. Phase keys are assigned by step_phases.
+# state): what each launch must read and write at least. Phase keys are
+# assigned by step_phases.
 def step_kernel_bytes(B, C=768, F=3072, V=50277):
     h = 2
     return [
@@ -696,8 +713,9 @@ def main():
     args = parse()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
-        print("bench.py measures one MI355X only: every chunk is independent and this build "
-              "has no multi-GPU path (see DESIGN.md, 'How it would shard'). Run with --gpus 1.",
+        print("bench.py measures one MI355X only: every chunk is independent, so the path "
+              "would shard as one process per GPU over chunk ranges, and this build runs one "
+              "GPU. Run with --gpus 1.",
               file=sys.stderr)
         sys.exit(2)
     if args.hbm_table:
